@@ -1,0 +1,216 @@
+"""Benchmark: paged GQA decode attention (Llama-3-8B shape) and stick relayout
+on one MI355X.  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (a "step"): one decode-attention step -- split-KV pass + merge pass --
+for batch 32, 32 q heads / 8 KV heads, head_dim 128, context 4096 per
+sequence, fp16 K/V ~ N(0,1) in 64-token stick-layout pages, block table a
+seeded permutation of the page pool.  Inputs are resident in HBM before the
+timed region; two KV caches (1.07 GB) alternate so the 256 MB last-level
+cache cannot serve a step from the previous one.
+
+Also timed (reported under "relayout"): fp16 [4096, 4096] -> sticks,
+sticks -> row-major, and transpose-restick, rotating 8 buffer pairs.
+
+Timing: HIP events on the stream the kernels are launched on, around K
+back-to-back steps, after W warm-up steps.  GB/s = algorithmic bytes / time.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak); relayout GB/s"
+PEAK_HBM_GBS = 8000.0
+B, HQ, HKV, D, CTX, PAGE, SPLIT = 32, 32, 8, 128, 4096, 64, 512
+
+
+def attn_bytes(B, Hq, Hkv, D, ctx_total, pages_total):
+    """Algorithmic HBM bytes of one decode step: K+V once, q, out, block
+    table, context lengths (split partials are not counted)."""
+    return ctx_total * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2 + 4 * pages_total + 4 * B
+
+
+def timed(fn, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per call
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(k_log_pages, v_log_pages, table, q, budget_s=12.0):
+    """The reference's CPU path: torch CPU eager fp32 SDPA over gathered pages
+    (oracle.attention), timed on the host cores for a bounded sample."""
+    import torch
+
+    from oracle import attention as OA
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    nthreads = torch.get_num_threads()
+    qs = q.float()
+    done_seq = 0
+    t0 = time.perf_counter()
+    t_sdpa = 0.0
+    while time.perf_counter() - t0 < budget_s:
+        b = done_seq % q.shape[0]
+        kb, vb = OA.gather_sequence(k_log_pages, v_log_pages, table[b], CTX)
+        kt = torch.from_numpy(kb).float()[None]
+        vt = torch.from_numpy(vb).float()[None]
+        s0 = time.perf_counter()
+        OA.sdpa_cpu_fp32(qs[b][None, :, None, :], kt, vt, scale=1 / math.sqrt(D))
+        t_sdpa += time.perf_counter() - s0
+        done_seq += 1
+    elapsed = time.perf_counter() - t0
+    seq_bytes = attn_bytes(1, HQ, HKV, D, CTX, CTX // PAGE)
+    return {
+        "value": round(seq_bytes * done_seq / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": f"{done_seq} of the workload's sequences (page gather + torch CPU fp32 SDPA), "
+                  f"{elapsed:.1f} s; SDPA alone {seq_bytes * done_seq / t_sdpa / 1e9:.3f} GB/s; "
+                  f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model()}",
+        "us_per_step_equiv": round(elapsed / done_seq * B * 1e6, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(this path has no multi-GPU component)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import torch_spyre_amd as tsa
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    seed = 0xAFFE
+
+    # ---------------- decode attention (the workload) ----------------
+    n_pages = B * CTX // PAGE
+    g = torch.Generator().manual_seed(seed)
+    gg = torch.Generator(device=dev).manual_seed(seed)
+    caches, tables = [], []
+    for r in range(2):
+        c = tsa.PagedKVCache(n_pages, HKV, D, device=dev, zero=False)
+        c.k.normal_(generator=gg)
+        c.v.normal_(generator=gg)
+        caches.append(c)
+        tables.append(torch.randperm(n_pages, generator=g).to(torch.int32).view(B, CTX // PAGE).to(dev))
+    q = torch.randn((B, HQ, D), generator=gg, device=dev).half()
+    lens = torch.full((B,), CTX, dtype=torch.int32, device=dev)
+    ws = torch.empty(tsa.workspace_bytes(B, HQ, HKV, D, CTX, SPLIT), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+
+    def step(i):
+        c = caches[i & 1]
+        tsa.paged_decode_attention(q, c.k, c.v, tables[i & 1], lens, split_tokens=SPLIT,
+                                   max_context_len=CTX, workspace=ws, out=out)
+
+    ms = timed(step, args.steps, args.warmup, stream)
+    nbytes = attn_bytes(B, HQ, HKV, D, B * CTX, n_pages)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    # ---------------- relayout (config: [4096, 4096] fp16) ----------------
+    R = C = 4096
+    nbuf = 8
+    xs = [torch.randint(-30000, 30000, (R, C), device=dev, dtype=torch.int16).view(torch.float16)
+          for _ in range(nbuf)]
+    dflt = tsa.SpyreTensorLayout([R, C], torch.float16)
+    trl = tsa.transpose_restick_layout(R, C)
+    devs = [tsa.to_device_layout(x, dflt) for x in xs]
+    outs_dev = [torch.empty_like(d) for d in devs]
+    outs_host = [torch.empty_like(x) for x in xs]
+    to_plan = tsa.dma_plan([R, C], [C, 1], [C, 1], 0, dflt, True)
+    from_plan = tsa.dma_plan([R, C], [C, 1], [C, 1], 0, dflt, False)
+    tr_plan = [tsa.restick_plan([R, C], dflt, trl)]
+    dma = tsa.relayout.dma_copy
+    rel_bytes = 2 * R * C * 2
+    relayout = {}
+    for name, fn in (
+        ("to_sticks", lambda i: dma(xs[i % nbuf], outs_dev[i % nbuf], to_plan)),
+        ("from_sticks", lambda i: dma(devs[i % nbuf], outs_host[i % nbuf], from_plan)),
+        ("transpose_restick", lambda i: dma(devs[i % nbuf], outs_dev[i % nbuf], tr_plan)),
+    ):
+        t = timed(fn, args.steps, args.warmup, stream)
+        relayout[name] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1),
+                          "frac": round(rel_bytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    # plain device copy of the same bytes, for reference
+    t = timed(lambda i: outs_host[i % nbuf].copy_(xs[i % nbuf]), args.steps, args.warmup, stream)
+    relayout["torch_copy_reference"] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1)}
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "Llama-3-8B-shaped paged GQA decode attention",
+                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": CTX,
+                   "page_tokens": PAGE, "split_tokens": SPLIT, "kv_dtype": "fp16"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decode_split_kernel + decode_merge_kernel (one step)",
+                     "algorithmic_bytes": nbytes},
+        "relayout": relayout,
+    }
+
+    if not args.no_cpu:
+        c = caches[0]
+        from oracle import attention as OA
+
+        k_log, v_log = OA.pages_to_logical(c.k.cpu().numpy(), c.v.cpu().numpy(), n_pages, HKV, D)
+        result["cpu_baseline"] = cpu_baseline(k_log, v_log, tables[0].cpu().numpy(), q.cpu())
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

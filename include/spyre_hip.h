@@ -1,0 +1,172 @@
+/*
+ * spyre_hip.h -- C ABI of the MI355X (gfx950) stick-relayout and paged
+ * decode-attention library (libspyre_hip.so).
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device addresses;
+ * `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ * Every entry point is asynchronous on `stream` and never allocates or frees
+ * device memory: the caller owns every buffer, including workspaces.
+ *
+ * Return codes: SPYRE_OK (0) or a negative SPYRE_E* code; the message of the
+ * last failure on the calling thread is available from spyre_last_error().
+ *
+ * Reference paths below are relative to the torch-spyre repository root.
+ */
+#ifndef SPYRE_HIP_H
+#define SPYRE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPYRE_ABI_VERSION 1
+
+#define SPYRE_OK 0
+#define SPYRE_EINVAL (-1)      /* bad argument (shape, stride, pointer)      */
+#define SPYRE_EUNSUPPORTED (-2) /* valid but not handled by a fast path       */
+#define SPYRE_ENOSPC (-3)      /* workspace / output buffer too small         */
+#define SPYRE_EHIP (-4)        /* a HIP runtime call failed                  */
+
+#define SPYRE_MAX_RANK 8       /* device rank of a layout: host rank <= 6, +1 */
+#define SPYRE_MAX_INFOS 64     /* loop nests per DMA description              */
+
+/* Device data formats on this path; names follow the reference's DataFormats
+ * (torch_spyre/csrc/module.cpp:295-316, torch_spyre/csrc/types_mapping.h:71-92). */
+#define SPYRE_FMT_INVALID 0
+#define SPYRE_FMT_SEN169_FP16 1
+#define SPYRE_FMT_IEEE_FP32 2
+#define SPYRE_FMT_IEEE_INT32 3
+
+/* Host element types, numbered as c10::ScalarType. */
+#define SPYRE_DT_INT32 3
+#define SPYRE_DT_INT64 4
+#define SPYRE_DT_FLOAT16 5
+#define SPYRE_DT_FLOAT32 6
+#define SPYRE_DT_BOOL 11
+#define SPYRE_DT_BFLOAT16 15
+
+/* One DMA loop nest (the reference's DataConversionStrideInfo,
+ * torch_spyre/csrc/spyre_mem.cpp:320-352).  Lists are innermost loop first;
+ * strides and offsets are in elements. */
+typedef struct spyre_stride_info {
+  int32_t rank;
+  int32_t reserved;
+  int64_t size[SPYRE_MAX_RANK];
+  int64_t stride_src[SPYRE_MAX_RANK];
+  int64_t stride_dst[SPYRE_MAX_RANK];
+  int64_t offset_src;
+  int64_t offset_dst;
+} spyre_stride_info;
+
+/* ---------------------------------------------------------------- misc -- */
+
+int spyre_abi_version(void);
+const char* spyre_last_error(void);
+
+/* --------------------------------------- layout descriptor (host only) -- */
+
+/* Device format of a host element type; SPYRE_FMT_INVALID if unsupported.
+ * Replaces stringToDTDataFormatPair (torch_spyre/csrc/types_mapping.h:63-113)
+ * as used by SpyreTensorLayout::init (torch_spyre/csrc/spyre_tensor_impl.cpp:141-144). */
+int spyre_device_format(int scalar_type);
+
+/* Elements per 128-byte stick of a device format, or -1.
+ * Replaces spyre::elems_per_stick (torch_spyre/csrc/spyre_tensor_impl.cpp:33-40). */
+int64_t spyre_elems_per_stick(int data_format);
+
+/* SpyreTensorLayout(host_size, host_strides, dtype, dim_order) and, with
+ * host_strides == NULL and dim_order == NULL, SpyreTensorLayout(host_size,
+ * dtype).  dim_order may carry a trailing -1 (sparse layout).  Writes
+ * device_rank entries to device_size/stride_map (capacity SPYRE_MAX_RANK).
+ * Replaces SpyreTensorLayout::init (torch_spyre/csrc/spyre_tensor_impl.cpp:124-179,
+ * bound at torch_spyre/csrc/module.cpp:229-232). */
+int spyre_stl_init(const int64_t* host_size, int host_rank, const int64_t* host_strides,
+                   int scalar_type, const int32_t* dim_order, int dim_order_len,
+                   int64_t* device_size, int64_t* stride_map, int* device_rank,
+                   int* data_format);
+
+/* 128 bytes x product(device_size[:-1]).
+ * Replaces get_device_size_in_bytes (torch_spyre/csrc/spyre_tensor_impl.cpp:286-292). */
+uint64_t spyre_device_size_in_bytes(const int64_t* device_size, int device_rank);
+
+/* DMA description of a host<->device relayout: the loop nests the reference
+ * hands to its DMA engine.  sizes/dma_strides/cpu_strides have host_rank
+ * entries.  Replaces get_device_stride_infos
+ * (torch_spyre/csrc/spyre_mem.cpp:176-354, called from generate_dci :363-440). */
+int spyre_dma_plan(const int64_t* sizes, const int64_t* dma_strides, const int64_t* cpu_strides,
+                   int host_rank, int64_t storage_offset, const int64_t* device_size,
+                   const int64_t* stride_map, int device_rank, int host2device,
+                   spyre_stride_info* infos, int max_infos, int* n_infos);
+
+/* Single loop nest moving a dense host tensor of host_size from device layout
+ * A to device layout B (both exact: no padding, no broadcast), i.e. the
+ * device-side restickify.  SPYRE_EUNSUPPORTED when the two tilings do not
+ * nest (the caller then relayouts through a host-layout buffer).
+ * Replaces the ReStickifyOpHBM program emitted for spyre::restickify
+ * (torch_spyre/_inductor/customops.py:338-342, lowering.py:803-833,
+ * codegen/superdsc.py:761-803). */
+int spyre_restick_plan(const int64_t* host_size, int host_rank,
+                       const int64_t* src_device_size, const int64_t* src_stride_map, int src_rank,
+                       const int64_t* dst_device_size, const int64_t* dst_stride_map, int dst_rank,
+                       spyre_stride_info* info);
+
+/* --------------------------------------------------------- GPU kernels -- */
+
+/* Executes DMA loop nests on the GPU: for every index tuple of every info,
+ * dst[offset_dst + i.stride_dst] = src[offset_src + i.stride_src], moving raw
+ * elem_bytes-sized elements (1, 2, 4 or 8; bit-exact).  Stick-preserving
+ * nests run as 16-byte vector copies, stick-transposing nests as 8x8
+ * register-transposed tiles.  Every nest is checked against src_bytes /
+ * dst_bytes before anything is launched.  Replaces the DMA launch of
+ * SpyreStream::copyAsyncImpl (torch_spyre/csrc/spyre_stream.cpp:190-210). */
+int spyre_dma_copy(const void* src, size_t src_bytes, void* dst, size_t dst_bytes, int elem_bytes,
+                   const spyre_stride_info* infos, int n_infos, void* stream);
+
+/* Batched KV-cache append into the paged stick-layout cache (relayout on
+ * write).  For every sequence b the new token goes to position
+ * positions[b]: page block_table[b*bt_stride + positions[b]/page_size],
+ * slot positions[b] % page_size; each table row holds pages_per_seq entries.
+ *   k_new, v_new : [B, Hkv, D] fp16, row-major
+ *   k_cache      : [num_pages, Hkv, D/64, page_size, 64] fp16 (sticks on D)
+ *   v_cache      : [num_pages, Hkv, D, page_size]      fp16 (sticks on tokens)
+ * Sequences with positions[b] < 0 are skipped; positions past the row and
+ * page ids outside [0, num_pages) are dropped (never written).  Replaces the per-offset
+ * spyre::overwrite programs (torch_spyre/_inductor/customops.py:260-308,
+ * tests/inductor/test_overwrite.py) with one launch whose offsets are data. */
+int spyre_kv_append_f16(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                        const int32_t* block_table, int64_t bt_stride, int64_t pages_per_seq,
+                        const int32_t* positions, int B, int Hkv, int D, int page_size,
+                        int64_t num_pages, void* stream);
+
+/* Workspace bytes needed by spyre_paged_decode_attn_f16. */
+size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv, int D, int max_context_len,
+                                               int split_tokens);
+
+/* Split-KV paged decode attention, one query token per sequence:
+ *   out[b,h,:] = softmax(scale * q[b,h,:] . K[b,h/g,t,:]^T) V[b,h/g,t,:],
+ *   t < context_lens[b], g = Hq / Hkv (GQA: q head h reads KV head h/g).
+ *   q, out       : [B, Hq, D] fp16 row-major
+ *   k_cache      : [num_pages, Hkv, D/64, page_size, 64] fp16 (sticks on D)
+ *   v_cache      : [num_pages, Hkv, D, page_size]      fp16 (sticks on tokens)
+ *   block_table  : int32, row b at block_table + b*bt_stride
+ *   context_lens : int32 [B]; every context_lens[b] <= max_context_len
+ *   lse          : optional fp32 [B, Hq] natural-log logsumexp (NULL to skip)
+ * D in {64, 128}, page_size 64, g <= 16, split_tokens a multiple of 64.
+ * Empty contexts give zeros (as torch's CPU SDPA does).  Replaces the SDPA
+ * overrideable decomposition (torch_spyre/_inductor/decompositions.py:523-609)
+ * selected by _fused_sdp_choice (torch_spyre/csrc/attn_utils.cpp:22-37). */
+int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* block_table, int64_t bt_stride,
+                                const int32_t* context_lens, void* out, float* lse,
+                                void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
+                                int D, int page_size, int64_t num_pages, int max_context_len,
+                                int split_tokens, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPYRE_HIP_H */

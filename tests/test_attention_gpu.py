@@ -1,0 +1,216 @@
+"""GPU parity of paged split-KV decode attention against the oracle.
+
+Bar (stated by the path's contract): fp16 outputs within max-abs 2e-3 and
+rel 1e-2 of torch's CPU eager SDPA in fp32 over the gathered pages.  The
+check is |gpu - ref| <= ATOL + RTOL * |ref| elementwise.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from tests.conftest import SEED
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-2
+
+
+def assert_close(got: torch.Tensor, ref: torch.Tensor):
+    got = got.float().cpu()
+    ref = ref.float().cpu()
+    assert got.shape == ref.shape
+    err = (got - ref).abs()
+    bound = ATOL + RTOL * ref.abs()
+    bad = err > bound
+    assert not torch.isnan(got).any(), "NaN in output"
+    assert not bad.any(), f"{int(bad.sum())} elements out of tolerance; max abs err {err.max():.3e}"
+
+
+def make_case(cuda, B, Hq, Hkv, D, ctx_lens, seed, extra_pages=3):
+    """Random paged cache (device layout, filled directly on the GPU), a
+    seeded random permutation of the page pool as block table, and q."""
+    import torch_spyre_amd as tsa
+
+    n_pages = [max(1, (c + 63) // 64) for c in ctx_lens]
+    W = max(n_pages)
+    pool = sum(n_pages) + extra_pages
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    table = torch.full((B, W), -1, dtype=torch.int32)
+    k = 0
+    for b, n in enumerate(n_pages):
+        table[b, :n] = perm[k:k + n]
+        k += n
+    gg = torch.Generator(device=cuda).manual_seed(seed)
+    cache = tsa.PagedKVCache(pool, Hkv, D, device=cuda, zero=False)
+    cache.k.normal_(generator=gg)
+    cache.v.normal_(generator=gg)
+    q = torch.randn((B, Hq, D), generator=gg, device=cuda, dtype=torch.float32).half()
+    lens = torch.tensor(ctx_lens, dtype=torch.int32)
+    return cache, table, lens, q
+
+
+def oracle_rows(cache, table, lens, q, rows, scale):
+    """Gathers only the pages the sampled rows use, converts them to logical
+    pages with the oracle's D2H, and runs torch CPU SDPA in fp32."""
+    table = table.cpu().numpy()
+    used = sorted({int(p) for b in rows for p in table[b][: max(1, (int(lens[b]) + 63) // 64)]})
+    remap = {p: i for i, p in enumerate(used)}
+    idx = torch.tensor(used, dtype=torch.long, device=cache.k.device)
+    kd = cache.k.index_select(0, idx).cpu().numpy()
+    vd = cache.v.index_select(0, idx).cpu().numpy()
+    k_log, v_log = OA.pages_to_logical(kd, vd, len(used), cache.Hkv, cache.D)
+    sub = np.full_like(table, -1)
+    for b in rows:
+        n = max(1, (int(lens[b]) + 63) // 64)
+        sub[b, :n] = [remap[int(p)] for p in table[b][:n]]
+    return OA.paged_decode_reference(q.cpu().float(), k_log, v_log, sub, lens.numpy(), scale, rows=rows)
+
+
+def run(cache, table, lens, q, cuda, **kw):
+    import torch_spyre_amd as tsa
+
+    return tsa.paged_decode_attention(q, cache.k, cache.v, table.to(cuda), lens.to(cuda), **kw)
+
+
+def test_config1_dense_mha_vs_cpu_sdpa(cuda):
+    """B=1, 8 heads MHA, D=64, ctx 512, contiguous fp16 q/k/v ~ N(0,1), scale 1/8."""
+    import torch_spyre_amd as tsa
+
+    g = torch.Generator().manual_seed(SEED)
+    q = torch.randn((1, 8, 1, 64), generator=g).half()
+    k = torch.randn((1, 8, 512, 64), generator=g).half()
+    v = torch.randn((1, 8, 512, 64), generator=g).half()
+    out = tsa.sdpa_decode(q.to(cuda), k.to(cuda), v.to(cuda), scale=0.125)
+    ref = OA.sdpa_cpu_fp32(q, k, v, scale=0.125)
+    assert_close(out, ref)
+    ref64 = torch.from_numpy(OA.sdpa_decomposition_fp64(q.numpy(), k.numpy(), v.numpy(), 0.125))
+    assert_close(out, ref64)
+
+
+@pytest.mark.parametrize("S", [1, 63, 64, 65, 200, 513])
+@pytest.mark.parametrize("D", [64, 128])
+def test_dense_gqa_ragged_lengths(cuda, S, D):
+    import torch_spyre_amd as tsa
+
+    g = torch.Generator().manual_seed(SEED + S + D)
+    q = torch.randn((2, 8, 1, D), generator=g).half()
+    k = torch.randn((2, 2, S, D), generator=g).half()
+    v = torch.randn((2, 2, S, D), generator=g).half()
+    out = tsa.sdpa_decode(q.to(cuda), k.to(cuda), v.to(cuda), enable_gqa=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
+
+
+def test_config3_llama3_8b_full(cuda):
+    """Batch 32, 32 q / 8 KV heads, D 128, ctx 4096, 64-token pages in a
+    permuted pool -- every row checked against the oracle."""
+    B, Hq, Hkv, D, ctx = 32, 32, 8, 128, 4096
+    cache, table, lens, q = make_case(cuda, B, Hq, Hkv, D, [ctx] * B, SEED)
+    out = run(cache, table, lens, q, cuda, max_context_len=ctx)
+    ref = oracle_rows(cache, table, lens, q, list(range(B)), 1 / math.sqrt(D))
+    assert_close(out, ref)
+
+
+@pytest.mark.parametrize("g", [1, 2, 4, 8, 16])
+def test_gqa_groups(cuda, g):
+    Hkv, D = 2, 128
+    lens = [1, 64, 100, 700, 1500]
+    cache, table, lens_t, q = make_case(cuda, len(lens), g * Hkv, Hkv, D, lens, SEED + g)
+    out = run(cache, table, lens_t, q, cuda, split_tokens=256)
+    ref = oracle_rows(cache, table, lens_t, q, list(range(len(lens))), 1 / math.sqrt(D))
+    assert_close(out, ref)
+
+
+def test_ragged_edges_and_empty(cuda):
+    """Contexts at page and split boundaries, and an empty context (zeros, as
+    torch's CPU SDPA returns)."""
+    lens = [0, 1, 63, 64, 65, 511, 512, 513, 1023, 1024, 1025, 4000]
+    cache, table, lens_t, q = make_case(cuda, len(lens), 32, 8, 128, lens, SEED + 99)
+    out, lse = run(cache, table, lens_t, q, cuda, return_lse=True)
+    rows = [b for b, c in enumerate(lens) if c > 0]
+    ref = oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128))
+    assert_close(out[rows], ref)
+    assert torch.count_nonzero(out[0]) == 0
+    assert torch.isinf(lse[0]).all()
+
+
+def test_lse_matches_oracle(cuda):
+    lens = [70, 900]
+    cache, table, lens_t, q = make_case(cuda, 2, 8, 2, 64, lens, SEED + 5)
+    scale = 0.3
+    out, lse = run(cache, table, lens_t, q, cuda, scale=scale, return_lse=True)
+    tab = table.numpy()
+    k_log, v_log = OA.pages_to_logical(cache.k.cpu().numpy(), cache.v.cpu().numpy(), cache.num_pages, 2, 64)
+    for b, c in enumerate(lens):
+        kb, _ = OA.gather_sequence(k_log, v_log, tab[b], c)
+        qb = q[b].cpu().double().numpy()  # [Hq, D]
+        kk = np.repeat(kb.astype(np.float64), 4, axis=0)  # [Hq, c, D]
+        s = scale * np.einsum("hd,htd->ht", qb, kk)
+        want = np.log(np.exp(s - s.max(1, keepdims=True)).sum(1)) + s.max(1)
+        assert np.allclose(lse[b].cpu().numpy(), want, atol=1e-3, rtol=1e-4)
+
+
+def test_split_invariance(cuda):
+    """Different split sizes (1 page .. whole context) agree within tolerance."""
+    lens = [3000, 2049, 77]
+    cache, table, lens_t, q = make_case(cuda, 3, 16, 4, 128, lens, SEED + 8)
+    base = run(cache, table, lens_t, q, cuda, split_tokens=4096)
+    for split in (64, 128, 512, 1024):
+        assert_close(run(cache, table, lens_t, q, cuda, split_tokens=split), base)
+
+
+def test_page_permutation_invariance_bitexact(cuda):
+    """Moving pages to other physical slots (and updating the table) gives
+    bit-identical output: the arithmetic follows logical token order only."""
+    lens = [1000, 333]
+    cache, table, lens_t, q = make_case(cuda, 2, 32, 8, 128, lens, SEED + 13)
+    out1 = run(cache, table, lens_t, q, cuda)
+    perm = torch.randperm(cache.num_pages, generator=torch.Generator().manual_seed(3))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(cache.num_pages)
+    cache.k.copy_(cache.k[perm.to(cuda)].clone())
+    cache.v.copy_(cache.v[perm.to(cuda)].clone())
+    table2 = torch.where(table >= 0, inv[table.clamp(min=0).long()].to(torch.int32), table)
+    out2 = run(cache, table2, lens_t, q, cuda)
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+
+
+def test_config4_ragged_full_shape_sampled(cuda):
+    """64 sequences, ctx ~ U[128, 32768] (seeded), 32/8 heads, D 128, split 512
+    with the merge on every sequence; six sampled rows against the oracle."""
+    g = torch.Generator().manual_seed(SEED)
+    lens = torch.randint(128, 32769, (64,), generator=g).tolist()
+    cache, table, lens_t, q = make_case(cuda, 64, 32, 8, 128, lens, SEED + 4)
+    out = run(cache, table, lens_t, q, cuda, split_tokens=512, max_context_len=32768)
+    rows = [0, 7, int(np.argmin(lens)), int(np.argmax(lens)), 40, 63]
+    ref = oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128))
+    assert_close(out[rows], ref)
+
+
+def test_bad_page_id_gives_nan_not_fault(cuda):
+    lens = [200]
+    cache, table, lens_t, q = make_case(cuda, 1, 4, 1, 64, lens, SEED + 21)
+    table[0, 1] = cache.num_pages + 1000  # out of range
+    out = run(cache, table, lens_t, q, cuda)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+
+
+def test_argument_errors(cuda):
+    import torch_spyre_amd as tsa
+
+    cache, table, lens_t, q = make_case(cuda, 1, 6, 4, 64, [100], SEED)
+    with pytest.raises(ValueError):
+        run(cache, table, lens_t, q, cuda)  # 6 % 4 != 0
+    cache, table, lens_t, q = make_case(cuda, 1, 4, 1, 64, [100], SEED)
+    with pytest.raises(ValueError):
+        run(cache, table, lens_t, q, cuda, max_context_len=10_000)  # table too short
+    with pytest.raises(ValueError):
+        run(cache, table, lens_t, q, cuda, workspace=torch.empty(4, dtype=torch.uint8, device=cuda))
+    with pytest.raises(tsa._lib.SpyreHipError):
+        run(cache, table, lens_t, q, cuda, split_tokens=100)

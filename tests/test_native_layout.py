@@ -1,0 +1,174 @@
+"""CPU: the native descriptor and DMA planner (libspyre_hip.so host code,
+called through the C ABI) against the golden vectors and the oracle.  No GPU
+kernel is launched here."""
+
+import copy
+import itertools
+import json
+import os
+import pickle
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layout as OL
+
+G = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "stl_golden.json")))
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def tsa():
+    import torch_spyre_amd
+
+    return torch_spyre_amd
+
+
+def test_library_exports_every_declared_symbol(tsa):
+    """Every function include/spyre_hip.h declares is exported and bound."""
+    hdr = open(os.path.join(ROOT, "include", "spyre_hip.h")).read()
+    declared = set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\*?\s+\*?(spyre_[a-z_0-9]+)\(", hdr, re.M))
+    assert len(declared) >= 12
+    from torch_spyre_amd import _lib
+
+    L = _lib.lib()
+    for name in declared:
+        assert hasattr(L, name), name
+        assert name in _lib.SIGNATURES, name
+    assert L.spyre_abi_version() == _lib.ABI_VERSION
+
+
+def test_default_layout_golden(tsa):
+    for c in G["default_layout"]:
+        s = tsa.SpyreTensorLayout(c["host_size"], torch.float16)
+        assert (s.device_size, s.stride_map) == (c["device_size"], c["stride_map"]), c
+
+
+def test_dim_order_golden(tsa):
+    for c in G["doc_default_layout"] + G["dim_order"] + G["sparse_dim_order"]:
+        strides = c.get("host_strides") or OL.contiguous_strides(c["host_size"])
+        s = tsa.SpyreTensorLayout(c["host_size"], strides, torch.float16, c["dim_order"])
+        assert (s.device_size, s.stride_map) == (c["device_size"], c["stride_map"]), c
+
+
+def test_str_eq_hash_pickle(tsa):
+    """tests/tensor/test_tensor_layout.py:106-150."""
+    s = tsa.SpyreTensorLayout([512, 256], torch.float16)
+    assert str(s) == G["str"]["expected"]
+    x = tsa.SpyreTensorLayout([512, 256], torch.float16)
+    y = tsa.SpyreTensorLayout([512, 256], [256, 1], torch.float16, [0, 1])
+    z = tsa.SpyreTensorLayout([512, 256], [256, 1], torch.float16, [1, 0])
+    z2 = tsa.SpyreTensorLayout([512, 256], torch.float32)
+    assert x == y and hash(x) == hash(y)
+    assert y != z and hash(y) != hash(z)
+    assert x != z2 and hash(x) != hash(z2)
+    assert {x: "value"}[y] == "value"
+    assert len({x, y, z}) == 2
+    assert pickle.loads(pickle.dumps(z)) == z
+    assert copy.deepcopy(z) == z
+    # explicit constructor equals the default one (test_tensor_layout.py:93-99)
+    e = tsa.SpyreTensorLayout([4, 512, 64], [64, 256, 1], tsa.get_device_dtype(torch.float16))
+    assert e == x
+    # older pickle versions load
+    st = z.__getstate__()
+    v2 = tsa.layout._from_state((2, st[1], st[2], st[3]))
+    v1 = tsa.layout._from_state((1, st[1], [0, 0, 0], st[2], st[3]))
+    assert v2 == z and v1 == z
+    with pytest.raises(ValueError):
+        tsa.layout._from_state((9, [], [], 1, 0))
+    assert z.elems_per_stick() == 64 and z2.elems_per_stick() == 32
+    assert s.device_size_in_bytes() == 4 * 512 * 128
+
+
+def _plans_equal(native, oracle):
+    a = [i.as_tuple() for i in native]
+    b = [(tuple(i.size), tuple(i.stride_src), tuple(i.stride_dst), i.offset_src, i.offset_dst) for i in oracle]
+    return a == b
+
+
+@pytest.mark.parametrize("case", G["explicit_roundtrip"], ids=lambda c: f"{c['kind']}-{c['sizes']}-{c['device_size']}")
+@pytest.mark.parametrize("h2d", [True, False])
+def test_dma_plans_equal_oracle_on_golden_layouts(tsa, case, h2d):
+    sizes, strides = list(case["sizes"]), list(case["strides"])
+    off = 0
+    if case["kind"] == "sliced_batch":
+        off = sizes[0] // 2
+        sizes = [sizes[0] - off]
+    lay = tsa.SpyreTensorLayout(case["device_size"], case["stride_map"], tsa.DataFormats.SEN169_FP16)
+    native = tsa.dma_plan(sizes, strides, strides, off, lay, h2d)
+    oracle = OL.device_stride_infos(sizes, strides, off, case["device_size"], case["stride_map"], h2d, strides)
+    assert _plans_equal(native, oracle)
+
+
+def test_dma_known_answer_native(tsa):
+    lay = tsa.SpyreTensorLayout([1024, 256], torch.float16)
+    (info,) = tsa.dma_plan([1024, 256], [256, 1], [256, 1], 0, lay, True)
+    size, ss, sd, _, _ = info.as_tuple()
+    ka = G["dma_known_answer"]
+    assert list(reversed(size)) == ka["loop_ranges"]
+    assert list(reversed(sd)) == ka["device_strides"]
+    assert list(reversed(ss)) == ka["host_strides"]
+
+
+def test_random_layouts_native_equals_oracle(tsa):
+    rng = np.random.default_rng(5)
+    for _ in range(300):
+        rank = int(rng.integers(1, 6))
+        sizes = [int(rng.choice([1, 2, 3, 40, 64, 65, 100, 128, 300])) for _ in range(rank)]
+        order = list(rng.permutation(rank))
+        if rng.random() < 0.2:
+            order = order + [-1]
+        strides = OL.contiguous_strides(sizes)
+        s = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+        o = OL.stl_init(sizes, strides, "float16", order)
+        assert (s.device_size, s.stride_map) == (o.device_size, o.stride_map), (sizes, order)
+        for h2d in (True, False):
+            try:
+                oracle = OL.device_stride_infos(sizes, strides, 0, o.device_size, o.stride_map, h2d, strides)
+            except RuntimeError:
+                with pytest.raises(Exception):
+                    tsa.dma_plan(sizes, strides, strides, 0, s, h2d)
+                continue
+            assert _plans_equal(tsa.dma_plan(sizes, strides, strides, 0, s, h2d), oracle), (sizes, order)
+
+
+def test_restick_plan_config2(tsa):
+    src = tsa.SpyreTensorLayout([4096, 4096], torch.float16)
+    dst = tsa.transpose_restick_layout(4096, 4096)
+    info = tsa.restick_plan([4096, 4096], src, dst)
+    size, ss, sd, _, _ = info.as_tuple()
+    # per host element (r, c): src offset and dst offset from the two plans
+    # must agree with the closed forms on a sample of elements
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        idx = [int(rng.integers(s)) for s in size]
+        so = sum(i * x for i, x in zip(idx, ss))
+        do = sum(i * x for i, x in zip(idx, sd))
+        # decode src offset (default sticks [C/64, R, 64]) -> (r, c)
+        t, rem = divmod(so, 4096 * 64)
+        r, k = divmod(rem, 64)
+        c = 64 * t + k
+        # dst (transposed sticks [R/64, C, 64]): dst[r // 64][c][r % 64]
+        assert do == (r // 64) * 4096 * 64 + c * 64 + r % 64
+
+
+def test_restick_plan_unsupported_returns_none(tsa):
+    # a layout with remainder splitting (folding) has no single-pass plan
+    a = tsa.SpyreTensorLayout([38, 64], [64, 1], tsa.DataFormats.SEN169_FP16)
+    b = tsa.SpyreTensorLayout([40, 60], torch.float16)
+    assert tsa.restick_plan([40, 60], a, b) is None
+
+
+def test_invalid_arguments_raise(tsa):
+    from torch_spyre_amd._lib import SpyreHipError
+
+    with pytest.raises(SpyreHipError):
+        tsa.SpyreTensorLayout([1, 2, 3, 4, 5, 6, 7], torch.float16)  # rank 7
+    with pytest.raises(SpyreHipError):
+        tsa.SpyreTensorLayout([4, 4], [4, 1], torch.float16, [0])  # dim_order length
+    with pytest.raises(TypeError):
+        tsa.SpyreTensorLayout([4, 4], torch.float64)
+    assert tsa.get_device_dtype(torch.float64) == tsa.DataFormats.INVALID
+    assert tsa.get_device_dtype(torch.bfloat16) == tsa.DataFormats.SEN169_FP16

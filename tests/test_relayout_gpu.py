@@ -1,0 +1,218 @@
+"""GPU parity of the stick relayouts against the oracle (bit-exact).
+
+Inputs are raw 16-bit patterns (finite fp16) compared as int16, so nothing
+goes through a float conversion.
+"""
+
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layout as OL
+from oracle import relayout as OR
+from oracle import kv as OK
+from tests.conftest import SEED
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "stl_golden.json")))
+
+
+def _bits_tensor(bits: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(bits.view(np.int16)).to(device).view(torch.float16)
+
+
+def _as_bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_config2_to_sticks_full(cuda):
+    import torch_spyre_amd as tsa
+
+    bits = OR.random_finite_f16_bits((4096, 4096), SEED)
+    x = _bits_tensor(bits, cuda)
+    stl = tsa.SpyreTensorLayout([4096, 4096], torch.float16)
+    assert stl.device_size == [64, 4096, 64] and stl.stride_map == [64, 4096, 1]
+    dev = tsa.to_device_layout(x, stl)
+    torch.cuda.synchronize()
+    assert np.array_equal(_as_bits(dev), OR.to_sticks(bits))
+
+
+def test_config2_from_sticks_full(cuda):
+    import torch_spyre_amd as tsa
+
+    bits = OR.random_finite_f16_bits((4096, 4096), SEED + 1)
+    stl = tsa.SpyreTensorLayout([4096, 4096], torch.float16)
+    dev = _bits_tensor(OR.to_sticks(bits), cuda)
+    host = tsa.from_device_layout(dev, stl, [4096, 4096])
+    torch.cuda.synchronize()
+    assert np.array_equal(_as_bits(host), bits)
+
+
+def test_config2_transpose_restick_full(cuda):
+    import torch_spyre_amd as tsa
+
+    bits = OR.random_finite_f16_bits((4096, 4096), SEED + 2)
+    x = _bits_tensor(bits, cuda)
+    src = tsa.SpyreTensorLayout([4096, 4096], torch.float16)
+    dst = tsa.transpose_restick_layout(4096, 4096)
+    assert dst.device_size == [64, 4096, 64] and dst.stride_map == [262144, 1, 4096]
+    want = OR.transpose_restick(bits)
+    # device -> device restickify (single pass)
+    dev = tsa.to_device_layout(x, src)
+    out = tsa.restickify(dev, dst)
+    # host order -> transposed sticks directly
+    out2 = tsa.to_device_layout(x, dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(_as_bits(out), want)
+    assert np.array_equal(_as_bits(out2), want)
+    # and back
+    back = tsa.from_device_layout(out, dst, [4096, 4096])
+    assert np.array_equal(_as_bits(back), bits)
+
+
+@pytest.mark.parametrize("case", GOLDEN["explicit_roundtrip"], ids=lambda c: f"{c['kind']}-{c['sizes']}-{c['device_size']}")
+def test_golden_explicit_layouts(cuda, case):
+    """Every explicit layout of tests/tensor/test_tensor_layout.py:193-405:
+    device bytes equal the oracle's H2D, and D2H restores the tensor."""
+    import torch_spyre_amd as tsa
+
+    sizes, strides = list(case["sizes"]), list(case["strides"])
+    span = 1 + sum((s - 1) * st for s, st in zip(sizes, strides))
+    store = OR.random_finite_f16_bits((span,), SEED + span)
+    off = 0
+    if case["kind"] == "sliced_batch":
+        off = sizes[0] // 2
+        sizes = [sizes[0] - off]
+    stl = tsa.SpyreTensorLayout(case["device_size"], case["stride_map"], tsa.DataFormats.SEN169_FP16)
+    base = _bits_tensor(store, cuda)
+    x = base.as_strided(sizes, strides, off)
+    dev = tsa.to_device_layout(x, stl)
+    want = OL.h2d(store, sizes, strides, off, OL.Layout(case["device_size"], case["stride_map"]))
+    got = _as_bits(dev).reshape(-1)
+    assert np.array_equal(got[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    ref = np.lib.stride_tricks.as_strided(store[off:], shape=sizes, strides=[s * 2 for s in strides])
+    assert np.array_equal(_as_bits(back).reshape(sizes), ref)
+
+
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(n):
+        rank = int(rng.integers(1, 5))
+        sizes = [int(rng.choice([1, 3, 40, 64, 65, 127, 128, 200])) for _ in range(rank)]
+        while np.prod(sizes) > 300_000:
+            sizes[int(rng.integers(rank))] = 3
+        orders = list(itertools.permutations(range(rank)))
+        order = list(orders[int(rng.integers(len(orders)))])
+        yield sizes, order
+
+
+@pytest.mark.parametrize("sizes,order", list(_random_cases(40, SEED)))
+def test_random_dim_orders_vs_oracle(cuda, sizes, order):
+    """Default/dim_order layouts of random shapes (padding, unit dims) vs the oracle."""
+    import torch_spyre_amd as tsa
+
+    strides = OL.contiguous_strides(sizes)
+    stl = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    o = OL.stl_init(sizes, strides, "float16", order)
+    assert (stl.device_size, stl.stride_map) == (o.device_size, o.stride_map)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + len(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    dev = tsa.to_device_layout(x, stl)
+    want = OL.h2d(bits, sizes, strides, 0, o)
+    assert np.array_equal(_as_bits(dev).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    assert np.array_equal(_as_bits(back).reshape(-1), bits)
+
+
+@pytest.mark.parametrize("sizes,order", list(_random_cases(24, SEED + 7)))
+def test_restickify_random_vs_oracle(cuda, sizes, order):
+    """D2D restickify from the default layout to a dim_order layout equals the
+    oracle's H2D(dst) of D2H(src), padding included."""
+    import torch_spyre_amd as tsa
+
+    strides = OL.contiguous_strides(sizes)
+    src = tsa.SpyreTensorLayout(sizes, torch.float16)
+    dst = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + 3 * len(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    out = tsa.restickify(tsa.to_device_layout(x, src), dst)
+    want = OL.h2d(bits, sizes, strides, 0, OL.stl_init(sizes, strides, "float16", order))
+    assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
+
+
+def test_page_layouts_vs_oracle(cuda):
+    """The paged K/V cache layouts built by the relayout engine equal the
+    oracle's H2D of the same logical pages."""
+    import torch_spyre_amd as tsa
+    from oracle import attention as OA
+
+    P, Hkv, D = 6, 2, 128
+    bits_k = OR.random_finite_f16_bits((P, Hkv, 64, D), SEED + 11)
+    bits_v = OR.random_finite_f16_bits((P, Hkv, 64, D), SEED + 12)
+    cache = tsa.PagedKVCache.from_pages(_bits_tensor(bits_k, cuda), _bits_tensor(bits_v, cuda))
+    wk, wv = OA.logical_to_pages(bits_k, bits_v)
+    assert np.array_equal(_as_bits(cache.k).reshape(-1), wk)
+    assert np.array_equal(_as_bits(cache.v).reshape(-1), wv)
+
+
+@pytest.mark.parametrize("shape,dims,offsets", [
+    ((1, 8, 64, 128), [2], [5]),
+    ((4, 8, 64, 128), [0, 2], [3, 63]),
+    ((3, 5, 7), [1], [2]),
+    ((64,), [0], [17]),
+])
+def test_overwrite_vs_oracle(cuda, shape, dims, offsets):
+    import torch_spyre_amd as tsa
+
+    out_bits = OR.random_finite_f16_bits(shape, SEED + 5)
+    in_shape = list(shape)
+    for d in dims:
+        in_shape[d] = 1 if shape[d] > 1 else shape[d]
+    if shape == (64,):
+        in_shape = [9]
+    in_bits = OR.random_finite_f16_bits(tuple(in_shape), SEED + 6)
+    out = _bits_tensor(out_bits, cuda)
+    inp = _bits_tensor(in_bits, cuda)
+    torch.ops.spyre.overwrite(inp, out, dims, offsets)
+    want = out_bits.copy()
+    OK.overwrite(in_bits, want, dims, offsets)
+    assert np.array_equal(_as_bits(out), want)
+
+
+def test_overwrite_sequential_kv_pattern(cuda):
+    """tests/inductor/test_overwrite.py:166-187: ten single-token writes into a
+    [1, 8, 64, 128] cache at dim 2, each at its own offset."""
+    import torch_spyre_amd as tsa
+
+    cache = torch.zeros((1, 8, 64, 128), dtype=torch.float16, device=cuda)
+    want = np.zeros((1, 8, 64, 128), dtype=np.uint16)
+    for i in range(10):
+        tok_bits = OR.random_finite_f16_bits((1, 8, 1, 128), SEED + 100 + i)
+        tsa.overwrite(_bits_tensor(tok_bits, cuda), cache, [2], [i])
+        OK.overwrite(tok_bits, want, [2], [i])
+    assert np.array_equal(_as_bits(cache), want)
+
+
+def test_empty_and_errors(cuda):
+    import torch_spyre_amd as tsa
+    from torch_spyre_amd._lib import SpyreHipError
+
+    x = torch.empty((0, 64), dtype=torch.float16, device=cuda)
+    stl = tsa.SpyreTensorLayout([0, 64], torch.float16)
+    dev = tsa.to_device_layout(x, stl)
+    assert tsa.from_device_layout(dev).shape == (0, 64)
+    # a loop nest past the end of the destination is refused on the host
+    src = torch.zeros(128, dtype=torch.float16, device=cuda)
+    dst = torch.zeros(64, dtype=torch.float16, device=cuda)
+    info = tsa._lib.StrideInfo()
+    info.rank, info.size[0], info.stride_src[0], info.stride_dst[0] = 1, 128, 1, 1
+    with pytest.raises(SpyreHipError):
+        tsa.relayout.dma_copy(src, dst, [info])
+    with pytest.raises(RuntimeError):
+        tsa.to_device_layout(torch.zeros(64, 64, dtype=torch.float16), stl)  # CPU tensor: no CPU path

@@ -1,0 +1,52 @@
+"""MI355X (gfx950) stick relayout and paged split-KV decode attention.
+
+A drop-in for torch-spyre's relayout / restickify / overwrite / decode-SDPA
+path: the SpyreTensorLayout descriptor, the host<->device DMA descriptors and
+the ``spyre::`` ops, executed by hand-written HIP kernels in
+``libspyre_hip.so`` (C ABI: include/spyre_hip.h).
+
+Importing the package loads the native library; it raises ImportError when
+the library is not built.  There is no CPU path.
+"""
+
+from . import _lib
+
+_lib.lib()  # fail loudly at import when the native library is missing
+
+from .layout import (  # noqa: E402
+    DataFormats,
+    ElementArrangement,
+    SpyreTensorLayout,
+    dma_plan,
+    get_device_dtype,
+    restick_plan,
+)
+from .relayout import (  # noqa: E402
+    copy_tensor,
+    device_tensor_layout,
+    from_device_layout,
+    overwrite,
+    restickify,
+    spyre_empty_with_layout,
+    to_device_layout,
+    transpose_restick_layout,
+)
+from .attention import (  # noqa: E402
+    PagedKVCache,
+    dense_to_pages,
+    k_page_layout,
+    kv_append,
+    paged_decode_attention,
+    sdpa_decode,
+    v_page_layout,
+    workspace_bytes,
+)
+from . import ops  # noqa: E402,F401  (registers the spyre:: ops)
+
+__all__ = [
+    "DataFormats", "ElementArrangement", "SpyreTensorLayout", "dma_plan", "get_device_dtype",
+    "restick_plan", "copy_tensor", "device_tensor_layout", "from_device_layout", "overwrite",
+    "restickify", "spyre_empty_with_layout", "to_device_layout", "transpose_restick_layout",
+    "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
+    "sdpa_decode", "v_page_layout", "workspace_bytes",
+]

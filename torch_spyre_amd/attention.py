@@ -1,0 +1,216 @@
+"""Paged split-KV decode attention and the stick-layout paged KV cache.
+
+The reference has no paged cache and no decode kernel: its SDPA is the
+overrideable decomposition (torch_spyre/_inductor/decompositions.py:523-609,
+selected by torch_spyre/csrc/attn_utils.cpp:22-37) and cache writes are
+``spyre::overwrite`` (torch_spyre/_inductor/customops.py:260-308).  This
+module keeps those semantics (softmax(scale q k^T) v, GQA q head h -> KV head
+h // g, empty context -> zeros) and adds the paged decode entry point.
+
+Page layouts, as SpyreTensorLayouts of the logical cache [num_pages, Hkv, 64, D]
+(page, KV head, token, feature):
+  K: device_size [P, Hkv, D/64, 64, 64], stride_map [Hkv*64*D, 64*D, 64, D, 1]
+     -- sticks along D (default tiling of each page);
+  V: device_size [P, Hkv, 1, D, 64],     stride_map [Hkv*64*D, 64*D, 64*D, 1, D]
+     -- sticks along tokens (transpose-restick of each page).
+Each (page, KV head) is 16 KiB contiguous in both.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .layout import DataFormats, SpyreTensorLayout
+from .relayout import _require_cuda, _stream_ptr, to_device_layout
+
+PAGE = 64
+
+
+def k_page_layout(num_pages: int, Hkv: int, D: int) -> SpyreTensorLayout:
+    return SpyreTensorLayout([num_pages, Hkv, D // 64, PAGE, 64],
+                             [Hkv * PAGE * D, PAGE * D, 64, D, 1], DataFormats.SEN169_FP16)
+
+
+def v_page_layout(num_pages: int, Hkv: int, D: int) -> SpyreTensorLayout:
+    return SpyreTensorLayout([num_pages, Hkv, 1, D, PAGE],
+                             [Hkv * PAGE * D, PAGE * D, PAGE * D, 1, D], DataFormats.SEN169_FP16)
+
+
+class PagedKVCache:
+    """fp16 paged KV cache in the stick layouts above."""
+
+    def __init__(self, num_pages: int, Hkv: int, D: int, device=None, zero: bool = True):
+        if D not in (64, 128):
+            raise ValueError("head_dim must be 64 or 128")
+        device = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        alloc = torch.zeros if zero else torch.empty
+        self.num_pages, self.Hkv, self.D = num_pages, Hkv, D
+        self.k = alloc((num_pages, Hkv, D // 64, PAGE, 64), dtype=torch.float16, device=device)
+        self.v = alloc((num_pages, Hkv, D, PAGE), dtype=torch.float16, device=device)
+        self.k_layout = k_page_layout(num_pages, Hkv, D)
+        self.v_layout = v_page_layout(num_pages, Hkv, D)
+
+    @classmethod
+    def from_pages(cls, k_pages: torch.Tensor, v_pages: torch.Tensor) -> "PagedKVCache":
+        """Builds the cache from logical pages [P, Hkv, 64, D] (token-major)
+        with the relayout engine."""
+        P, Hkv, T, D = k_pages.shape
+        if T != PAGE or v_pages.shape != k_pages.shape:
+            raise ValueError("pages must be [P, Hkv, 64, D] for both K and V")
+        self = cls.__new__(cls)
+        self.num_pages, self.Hkv, self.D = P, Hkv, D
+        self.k_layout = k_page_layout(P, Hkv, D)
+        self.v_layout = v_page_layout(P, Hkv, D)
+        self.k = to_device_layout(k_pages, self.k_layout).view(P, Hkv, D // 64, PAGE, 64)
+        self.v = to_device_layout(v_pages, self.v_layout).view(P, Hkv, D, PAGE)
+        return self
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, block_table: torch.Tensor,
+               positions: torch.Tensor) -> None:
+        kv_append(k_new, v_new, self.k, self.v, block_table, positions)
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, Hkv: int, D: int) -> int:
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_cuda(t, name)
+        if t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous float16")
+    per_page = Hkv * D * PAGE
+    if k_cache.numel() % per_page or k_cache.numel() != v_cache.numel():
+        raise ValueError(f"caches must hold whole pages of {per_page} elements (Hkv={Hkv}, D={D})")
+    if k_cache.dim() >= 2 and k_cache.shape[1] != Hkv:
+        raise ValueError(f"k_cache has {k_cache.shape[1]} KV heads, expected {Hkv}")
+    return k_cache.numel() // per_page
+
+
+def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+              v_cache: torch.Tensor, block_table: torch.Tensor, positions: torch.Tensor) -> None:
+    """Writes token positions[b] of every sequence b (k_new/v_new [B, Hkv, D])
+    into its page slot, in one launch.  positions[b] < 0 skips b."""
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        _require_cuda(t, name)
+        if t.dtype != torch.float16 or t.dim() != 3 or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous float16 [B, Hkv, D]")
+    B, Hkv, D = k_new.shape
+    if v_new.shape != k_new.shape:
+        raise ValueError("k_new and v_new shapes differ")
+    num_pages = _check_cache(k_cache, v_cache, Hkv, D)
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
+            or block_table.stride(1) != 1:
+        raise ValueError("block_table must be int32 [B, pages_per_seq] with unit column stride")
+    if positions.dtype != torch.int32 or positions.shape != (B,) or not positions.is_contiguous():
+        raise ValueError("positions must be contiguous int32 [B]")
+    rc = _lib.lib().spyre_kv_append_f16(k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(),
+                                        v_cache.data_ptr(), block_table.data_ptr(),
+                                        block_table.stride(0), block_table.shape[1],
+                                        positions.data_ptr(), B, Hkv, D,
+                                        PAGE, num_pages, _stream_ptr(k_new.device))
+    _lib.check("spyre_kv_append_f16", rc)
+
+
+def workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_context_len: int, split_tokens: int = 512) -> int:
+    return int(_lib.lib().spyre_paged_decode_attn_workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens))
+
+
+def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           block_table: torch.Tensor, context_lens: torch.Tensor,
+                           scale: Optional[float] = None, split_tokens: int = 512,
+                           max_context_len: Optional[int] = None,
+                           workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                           return_lse: bool = False):
+    """out[b, h] = softmax(scale * q[b, h] . K[b, h // g]^T) V[b, h // g] over
+    the first context_lens[b] tokens of sequence b's pages.
+
+    q [B, Hq, D] fp16; caches as PagedKVCache; block_table int32 [B, W];
+    context_lens int32 [B].  ``max_context_len`` bounds every context (if
+    omitted it is read from context_lens, which synchronises)."""
+    _require_cuda(q, "q")
+    if q.dtype != torch.float16 or q.dim() != 3 or not q.is_contiguous():
+        raise ValueError("q must be contiguous float16 [B, Hq, D]")
+    B, Hq, D = q.shape
+    Hkv = k_cache.shape[1]
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    num_pages = _check_cache(k_cache, v_cache, Hkv, D)
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
+            or block_table.stride(1) != 1 or not block_table.is_cuda:
+        raise ValueError("block_table must be a CUDA int32 [B, W] tensor with unit column stride")
+    if context_lens.dtype != torch.int32 or context_lens.shape != (B,) or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be contiguous int32 [B]")
+    if max_context_len is None:
+        max_context_len = int(context_lens.max().item()) if B else 0
+    if max_context_len > block_table.shape[1] * PAGE:
+        raise ValueError(f"max_context_len {max_context_len} exceeds the block table's "
+                         f"{block_table.shape[1]} pages")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    need = workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens)
+    if workspace is None:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, need {need}")
+    if out is None:
+        out = torch.empty_like(q)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
+    rc = _lib.lib().spyre_paged_decode_attn_f16(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+        block_table.stride(0), context_lens.data_ptr(), out.data_ptr(),
+        lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, PAGE, num_pages,
+        max_context_len, split_tokens, scale, _stream_ptr(q.device))
+    _lib.check("spyre_paged_decode_attn_f16", rc)
+    return (out, lse) if return_lse else out
+
+
+def dense_to_pages(k: torch.Tensor, v: torch.Tensor) -> tuple[PagedKVCache, torch.Tensor]:
+    """Dense K/V [B, Hkv, S, D] -> paged cache (sequence b's page p is page
+    b*P + p) and its block table.  Each tensor is moved in one relayout pass:
+    the strided view [B, P, Hkv, 64, D] of the dense tensor is laid out with
+    the page layouts (K keeps its sticks on D, V is transpose-resticked onto
+    tokens).  Tokens past S are zero."""
+    B, Hkv, S, D = k.shape
+    P = max(1, (S + PAGE - 1) // PAGE)
+    S2 = P * PAGE
+    if S2 != S:
+        k = torch.nn.functional.pad(k, (0, 0, 0, S2 - S))
+        v = torch.nn.functional.pad(v, (0, 0, 0, S2 - S))
+    k, v = k.contiguous(), v.contiguous()
+    k5 = k.view(B, Hkv, P, PAGE, D).permute(0, 2, 1, 3, 4)  # [B, P, Hkv, 64, D]
+    v5 = v.view(B, Hkv, P, PAGE, D).permute(0, 2, 1, 3, 4)
+    k_lay = SpyreTensorLayout([B, P, Hkv, D // 64, PAGE, 64],
+                              [Hkv * S2 * D, PAGE * D, S2 * D, 64, D, 1], DataFormats.SEN169_FP16)
+    v_lay = SpyreTensorLayout([B, P, Hkv, 1, D, PAGE],
+                              [Hkv * S2 * D, PAGE * D, S2 * D, PAGE * D, 1, D], DataFormats.SEN169_FP16)
+    cache = PagedKVCache.__new__(PagedKVCache)
+    cache.num_pages, cache.Hkv, cache.D = B * P, Hkv, D
+    cache.k_layout = k_page_layout(B * P, Hkv, D)
+    cache.v_layout = v_page_layout(B * P, Hkv, D)
+    cache.k = to_device_layout(k5, k_lay).view(B * P, Hkv, D // 64, PAGE, 64)
+    cache.v = to_device_layout(v5, v_lay).view(B * P, Hkv, D, PAGE)
+    table = torch.arange(B * P, dtype=torch.int32, device=k.device).view(B, P)
+    return cache, table
+
+
+def sdpa_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                scale: Optional[float] = None, enable_gqa: bool = False,
+                split_tokens: int = 512) -> torch.Tensor:
+    """F.scaled_dot_product_attention for one query token (Sq == 1), no mask,
+    no dropout: query [B, Hq, 1, D], key/value [B, Hkv, S, D] fp16 ->
+    [B, Hq, 1, D].  Dense K/V are relaid into pages first (as the reference's
+    compiler restickifies K^T for its SDPA), then the paged kernel runs."""
+    if query.dim() != 4 or query.shape[2] != 1:
+        raise ValueError("sdpa_decode handles exactly one query token: query [B, Hq, 1, D]")
+    B, Hq, _, D = query.shape
+    Bk, Hkv, S, Dk = key.shape
+    if value.shape != key.shape or Bk != B or Dk != D:
+        raise ValueError("key/value must be [B, Hkv, S, D] matching query")
+    if Hq != Hkv and not enable_gqa:
+        raise ValueError("Hq != Hkv requires enable_gqa=True")
+    cache, table = dense_to_pages(key.to(torch.float16), value.to(torch.float16))
+    lens = torch.full((B,), S, dtype=torch.int32, device=query.device)
+    out = paged_decode_attention(query[:, :, 0, :].to(torch.float16).contiguous(), cache.k, cache.v,
+                                 table, lens, scale=scale, split_tokens=split_tokens, max_context_len=S)
+    return out.unsqueeze(2)
