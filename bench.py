@@ -110,6 +110,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--split", type=int, default=SPLIT, help="tokens per KV split (multiple of 64)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -138,12 +139,13 @@ def main():
         tables.append(torch.randperm(n_pages, generator=g).to(torch.int32).view(B, CTX // PAGE).to(dev))
     q = torch.randn((B, HQ, D), generator=gg, device=dev).half()
     lens = torch.full((B,), CTX, dtype=torch.int32, device=dev)
-    ws = torch.empty(tsa.workspace_bytes(B, HQ, HKV, D, CTX, SPLIT), dtype=torch.uint8, device=dev)
+    split = args.split
+    ws = torch.empty(tsa.workspace_bytes(B, HQ, HKV, D, CTX, split), dtype=torch.uint8, device=dev)
     out = torch.empty_like(q)
 
     def step(i):
         c = caches[i & 1]
-        tsa.paged_decode_attention(q, c.k, c.v, tables[i & 1], lens, split_tokens=SPLIT,
+        tsa.paged_decode_attention(q, c.k, c.v, tables[i & 1], lens, split_tokens=split,
                                    max_context_len=CTX, workspace=ws, out=out)
 
     ms = timed(step, args.steps, args.warmup, stream)
@@ -195,7 +197,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "Llama-3-8B-shaped paged GQA decode attention",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": CTX,
-                   "page_tokens": PAGE, "split_tokens": SPLIT, "kv_dtype": "fp16"},
+                   "page_tokens": PAGE, "split_tokens": split, "kv_dtype": "fp16"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": "decode_split_kernel + decode_merge_kernel (one step)",

@@ -186,7 +186,7 @@ def test_config4_ragged_full_shape_sampled(cuda):
     g = torch.Generator().manual_seed(SEED)
     lens = torch.randint(128, 32769, (64,), generator=g).tolist()
     cache, table, lens_t, q = make_case(cuda, 64, 32, 8, 128, lens, SEED + 4)
-    out = run(cache, table, lens_t, q, cuda, split_tokens=512, max_context_len=32768)
+    out = run(cache, table, lens_t, q, cuda, split_tokens=512, max_context_len=max(lens))
     rows = [0, 7, int(np.argmin(lens)), int(np.argmax(lens)), 40, 63]
     ref = oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128))
     assert_close(out[rows], ref)

@@ -64,6 +64,75 @@ struct SplitArgs {
   float scale_log2;
 };
 
+// ---- Operand loads: whole cache lines, then a lane shuffle --------------
+//
+// An MFMA 16x16x32 operand gives each row 4 lanes x 16 B = 64 B per
+// instruction, i.e. half of a 128-byte stick; loading operands directly
+// would make every load instruction touch 16 half lines.  Instead each
+// instruction reads 8 whole sticks (8 lanes per stick) and two such loads X
+// (rows 0-7) and Y (rows 8-15) are turned into the two operands of the
+// stick's halves:
+//   X lane l: row l&7,     chunk (l&8) ? 4 + (l>>4) : (l>>4)
+//   Y lane l: row 8+(l&7), chunk (l&8) ? (l>>4) : 4 + (l>>4)
+//   op0 = bit3 ? Y : X                 -> lane l: row l&15, chunk l>>4
+//   op1 = ror8(bit3 ? X : Y)           -> lane l: row l&15, chunk 4 + (l>>4)
+// where ror8 is the DPP row rotation by 8 (lane l reads lane l^8 of its
+// 16-lane row).  A chunk is 16 B = 8 halves of the row.
+
+__device__ __forceinline__ f16x8 ror8(f16x8 x) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 v = __builtin_bit_cast(i32x4, x);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = __builtin_amdgcn_mov_dpp(v[i], 0x128, 0xf, 0xf, false);
+  return __builtin_bit_cast(f16x8, v);
+}
+
+__device__ __forceinline__ int chunk_x(int lane) { return (lane & 8) ? 4 + (lane >> 4) : (lane >> 4); }
+__device__ __forceinline__ int chunk_y(int lane) { return (lane & 8) ? (lane >> 4) : 4 + (lane >> 4); }
+
+// Builds the operand pair from the raw X / Y loads (in place).
+__device__ __forceinline__ void shuffle_pair(f16x8& x, f16x8& y, bool bit3) {
+  const f16x8 op0 = bit3 ? y : x;
+  const f16x8 op1 = ror8(bit3 ? x : y);
+  x = op0;
+  y = op1;
+}
+
+// QK block jh = (j, h): MFMA row i <-> token 32j + 8(i/4) + 4h + i%4.
+__device__ __forceinline__ int qk_token(int jh, int i) {
+  return 32 * (jh >> 1) + 8 * (i >> 2) + 4 * (jh & 1) + (i & 3);
+}
+
+// Raw K loads of one page: for block jh and stick tile t, X -> ka[jh][2t],
+// Y -> ka[jh][2t+1] (operands after shuffle_pair: d = 32 ds + 8 (l>>4)).
+template <int D>
+__device__ __forceinline__ void load_k(f16x8 (&ka)[4][D / 32], const _Float16* kp, int lane) {
+  const int cx = chunk_x(lane), cy = chunk_y(lane), r = lane & 7;
+#pragma unroll
+  for (int jh = 0; jh < 4; ++jh) {
+    const int tx = qk_token(jh, r), ty = qk_token(jh, 8 + r);
+#pragma unroll
+    for (int t = 0; t < D / 64; ++t) {
+      const _Float16* tile = kp + t * (kPage * 64);
+      ka[jh][2 * t] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(tile + tx * 64 + cx * 8));
+      ka[jh][2 * t + 1] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(tile + ty * 64 + cy * 8));
+    }
+  }
+}
+
+// Raw V^T loads of one page: for d block db, X (d rows 16db + 0..7) ->
+// va[db][0], Y (rows 16db + 8..15) -> va[db][1]; after shuffle_pair
+// va[db][j] is the operand for tokens 32j + 8 (l>>4) .. +8.
+template <int D>
+__device__ __forceinline__ void load_v(f16x8 (&va)[D / 16][2], const _Float16* vp, int lane) {
+  const int cx = chunk_x(lane), cy = chunk_y(lane), r = lane & 7;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    va[db][0] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vp + (16 * db + r) * kPage + cx * 8));
+    va[db][1] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vp + (16 * db + 8 + r) * kPage + cy * 8));
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(SplitArgs a) {
   constexpr int DS = D / 32;  // QK K-steps
@@ -76,6 +145,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(SplitArgs a) 
   const int p1 = min(p0 + a.split_pages, n_pages);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int col = lane & 15, grp = lane >> 4;
+  // This wavefront's pages: p0 + wave + kWaves * it, it < n_it.
+  const int n_it = (p1 - p0 - wave + kWaves - 1) / kWaves;
+  const int32_t* trow = a.block_table + static_cast<int64_t>(b) * a.bt_stride + p0 + wave;
+  // One lane per page: the page ids of the next 64 iterations.
+  int ids = lane < n_it ? trow[kWaves * lane] : 0;
 
   // Q^T operand: lane = (head col, d group grp); padded heads are zero.
   f16x8 qb[DS];
@@ -97,88 +171,99 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(SplitArgs a) 
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int p = p0 + wave; p < p1; p += kWaves) {
-    int64_t phys = a.block_table[static_cast<int64_t>(b) * a.bt_stride + p];
-    const bool bad_page = phys < 0 || phys >= a.num_pages;
-    if (bad_page) phys = 0;  // stay in bounds; the result is poisoned below
-    poisoned |= bad_page;
-    const _Float16* kp = a.k + phys * page_elems + kvh * head_elems;
-    const _Float16* vp = a.v + phys * page_elems + kvh * head_elems;
-    const int valid = min(kPage, ctx - p * kPage);
-
-    // K operands: block jh = (j, h); row col <-> token 32j + 8(col/4) + 4h + col%4.
+  if (n_it > 0) {
+    // Page it's K/V base pointers (page id broadcast from lane it % 64).
+    auto locate = [&](int it, const _Float16*& kp, const _Float16*& vp) {
+      int64_t phys = __builtin_amdgcn_readlane(ids, it & 63);
+      const bool bad = phys < 0 || phys >= a.num_pages;
+      poisoned |= bad;
+      if (bad) phys = 0;  // stay in bounds; the result is poisoned below
+      kp = a.k + phys * page_elems + kvh * head_elems;
+      vp = a.v + phys * page_elems + kvh * head_elems;
+    };
+    const _Float16 *kp, *vp;
+    locate(0, kp, vp);
     f16x8 ka[4][DS];
-#pragma unroll
-    for (int jh = 0; jh < 4; ++jh) {
-      const int t = 32 * (jh >> 1) + 8 * (col >> 2) + 4 * (jh & 1) + (col & 3);
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const int d = 32 * ds + 8 * grp;
-        ka[jh][ds] = *reinterpret_cast<const f16x8*>(kp + (d >> 6) * (kPage * 64) + t * 64 + (d & 63));
-      }
-    }
-    // V operands: V^T[d = 16db + col][tokens 32j + 8grp .. +8].
     f16x8 va[DB][2];
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        va[db][j] = *reinterpret_cast<const f16x8*>(vp + (16 * db + col) * kPage + 32 * j + 8 * grp);
+    load_k<D>(ka, kp, lane);
+    load_v<D>(va, vp, lane);
 
-    f32x4 sc[4];
+    for (int it = 0; it < n_it; ++it) {
+      const int valid = min(kPage, ctx - (p0 + wave + kWaves * it) * kPage);
+      const bool bit3 = (lane & 8) != 0;
 #pragma unroll
-    for (int jh = 0; jh < 4; ++jh) {
-      sc[jh] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds)
-        sc[jh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[ds], sc[jh], 0, 0, 0);
-    }
+        for (int t = 0; t < DS / 2; ++t) shuffle_pair(ka[jh][2 * t], ka[jh][2 * t + 1], bit3);
+      f32x4 sc[4];
+#pragma unroll
+      for (int jh = 0; jh < 4; ++jh) {
+        sc[jh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+          sc[jh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[ds], sc[jh], 0, 0, 0);
+      }
+      // The K registers are consumed: start the next page's K loads now, so
+      // they are in flight during this page's softmax and PV.
+      const bool more = it + 1 < n_it;
+      if (more) {
+        if (((it + 1) & 63) == 0) {
+          const int nx = it + 1 + lane;
+          ids = nx < n_it ? trow[kWaves * nx] : 0;
+        }
+        locate(it + 1, kp, vp);
+        load_k<D>(ka, kp, lane);
+      }
 
-    // This lane now holds head col's scores for tokens 32j + 8grp + 4h + v.
-    float mx = -INFINITY;
+      // This lane holds head col's scores for tokens 32j + 8grp + 4h + v.
+      float mx = -INFINITY;
 #pragma unroll
-    for (int jh = 0; jh < 4; ++jh)
+      for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int t = 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
-        const float x = t < valid ? sc[jh][v] * a.scale_log2 : -INFINITY;
-        sc[jh][v] = x;
-        mx = fmaxf(mx, x);
+        for (int v = 0; v < 4; ++v) {
+          const int t = 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
+          const float x = t < valid ? sc[jh][v] * a.scale_log2 : -INFINITY;
+          sc[jh][v] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, wave_xor(mx, 16));
+      mx = fmaxf(mx, wave_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      float psum = 0.f;
+      f16x8 pb[2];
+#pragma unroll
+      for (int jh = 0; jh < 4; ++jh)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float pv = fast_exp2(sc[jh][v] - m_new);
+          psum += pv;
+          pb[jh >> 1][(jh & 1) * 4 + v] = static_cast<_Float16>(pv);
+        }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) shuffle_pair(va[db][0], va[db][1], bit3);
+      if (valid < kPage) {
+        // Tokens past the context may hold any bits (even NaN); zero them so
+        // that 0 * V stays 0 in the PV product.
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (32 * j + 8 * grp + e >= valid) va[db][j][e] = static_cast<_Float16>(0.f);
       }
-    mx = fmaxf(mx, wave_xor(mx, 16));
-    mx = fmaxf(mx, wave_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
-    float psum = 0.f;
-    f16x8 pb[2];
-#pragma unroll
-    for (int jh = 0; jh < 4; ++jh)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float pv = fast_exp2(sc[jh][v] - m_new);
-        psum += pv;
-        pb[jh >> 1][(jh & 1) * 4 + v] = static_cast<_Float16>(pv);
-      }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) o[db] *= alpha;
-    if (valid < kPage) {
-      // Tokens past the context may hold any bits (even NaN); zero them so
-      // that 0 * V stays 0 in the PV product.
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (32 * j + 8 * grp + e >= valid) va[db][j][e] = static_cast<_Float16>(0.f);
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
+      if (more) load_v<D>(va, vp, lane);
     }
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
-    m_run = m_new;
   }
   if (poisoned) l_run = NAN;  // propagates to the merged output: NaN, not a fault
 
@@ -229,7 +314,30 @@ struct MergeArgs {
 };
 
 template <int D>
+__device__ __forceinline__ float block_reduce(float x, bool is_max, float* scratch) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float y = __shfl_xor(x, m, 64);
+    x = is_max ? fmaxf(x, y) : x + y;
+  }
+  const int w = threadIdx.x / 64;
+  if ((threadIdx.x & 63) == 0) scratch[w] = x;
+  __syncthreads();
+  float r = scratch[0];
+#pragma unroll
+  for (int i = 1; i < D / 64; ++i) r = is_max ? fmaxf(r, scratch[i]) : r + scratch[i];
+  __syncthreads();
+  return r;
+}
+
+// Split-KV merge: one block of D threads per (q head, sequence).  The splits'
+// weights exp2(m_s - M) are computed once per chunk of D splits into LDS,
+// then each thread (one output feature) sums its column with 8-way unrolled
+// independent loads.
+template <int D>
 __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
+  __shared__ float s_w[D];
+  __shared__ float s_red[D / 64];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int kvh = h / a.g, hh = h % a.g;
   const int ctx_raw = a.ctx_lens[b];
@@ -242,16 +350,39 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
     return;
   }
   const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits;
-  const float* wo = a.ws + slot0 * a.g * D;
-  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + slot0 * a.g * 2;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, wm[(s * a.g + hh) * 2]);
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float f = fast_exp2(wm[(s * a.g + hh) * 2] - M);
-    L += wm[(s * a.g + hh) * 2 + 1] * f;
-    acc += wo[(s * a.g + hh) * D + d] * f;
+  const float* wo = a.ws + slot0 * a.g * D + hh * D + d;
+  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + slot0 * a.g * 2 + hh * 2;
+  const int64_t so = static_cast<int64_t>(a.g) * D;  // split stride of wo
+  const int sm = 2 * a.g;                              // split stride of wm
+
+  float mx = -INFINITY;
+  for (int s = d; s < ns; s += D) mx = fmaxf(mx, wm[s * sm]);
+  const float M = block_reduce<D>(mx, true, s_red);
+
+  float acc = 0.f, lpart = 0.f;
+  for (int c = 0; c < ns; c += D) {
+    const int s = c + d;
+    float w = 0.f;
+    if (s < ns) {
+      w = fast_exp2(wm[s * sm] - M);
+      lpart += wm[s * sm + 1] * w;
+    }
+    s_w[d] = w;
+    __syncthreads();
+    const int n = min(D, ns - c);
+    const float* col = wo + c * so;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = col[(j + u) * so];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += x[u] * s_w[j + u];
+    }
+    for (; j < n; ++j) acc += col[j * so] * s_w[j];
+    __syncthreads();
   }
+  const float L = block_reduce<D>(lpart, false, s_red);
   float r = acc / L;
   if (ctx_raw > a.max_ctx) r = NAN;  // caller broke the max_context_len contract
   o[d] = static_cast<_Float16>(r);
