@@ -32,6 +32,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak); relayout GB/s"
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per decode_split_kernel launch at split 512, from rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the same counters on
+# a 32 MiB copy kernel (x1.997 and x0.999): 538.3 MB read + 4.2 MB written.
+TRAFFIC_BYTES = 542_500_000
 B, HQ, HKV, D, CTX, PAGE, SPLIT = 32, 32, 8, 128, 4096, 64, 512
 
 
@@ -143,14 +147,28 @@ def main():
     ws = torch.empty(tsa.workspace_bytes(B, HQ, HKV, D, CTX, split), dtype=torch.uint8, device=dev)
     out = torch.empty_like(q)
 
-    def step(i):
-        c = caches[i & 1]
-        tsa.paged_decode_attention(q, c.k, c.v, tables[i & 1], lens, split_tokens=split,
-                                   max_context_len=CTX, workspace=ws, out=out)
+    # One step = split pass + merge pass.  Events before and after each split
+    # launch (same stream) give the dominant kernel's own duration.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
 
-    ms = timed(step, args.steps, args.warmup, stream)
+    calls = [tsa.PagedDecode(q, c.k, c.v, t, lens, split_tokens=split, max_context_len=CTX,
+                             workspace=ws, out=out) for c, t in zip(caches, tables)]
+
+    def step(i, record=False):
+        call = calls[i & 1]
+        if record:
+            ev[i][0].record(stream)
+        call.split()
+        if record:
+            ev[i][1].record(stream)
+        call.merge()
+
+    ms = timed(lambda i: step(i, True), args.steps, args.warmup, stream)
+    split_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
     nbytes = attn_bytes(B, HQ, HKV, D, B * CTX, n_pages)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    split_gbs = nbytes / (split_ms * 1e-3) / 1e9
 
     # ---------------- relayout (config: [4096, 4096] fp16) ----------------
     R = C = 4096
@@ -198,9 +216,9 @@ def main():
         "config": {"workload": "Llama-3-8B-shaped paged GQA decode attention",
                    "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": CTX,
                    "page_tokens": PAGE, "split_tokens": split, "kv_dtype": "fp16"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "decode_split_kernel + decode_merge_kernel (one step)",
+        "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(split_gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,
+                     "kernel": "decode_split_kernel<128>", "kernel_us": round(split_ms * 1e3, 2),
                      "algorithmic_bytes": nbytes},
         "relayout": relayout,
     }

@@ -165,6 +165,23 @@ int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* 
                                 int D, int page_size, int64_t num_pages, int max_context_len,
                                 int split_tokens, float scale, void* stream);
 
+/* The two passes of spyre_paged_decode_attn_f16, for callers that schedule
+ * them separately (same arguments and workspace; the merge pass reads what
+ * the split pass wrote).  Pass 1 writes per-split partials (unnormalised O,
+ * running max, row sum) to the workspace; pass 2 combines them into out/lse.
+ * No reference counterpart: the reference's SDPA decomposition
+ * (torch_spyre/_inductor/decompositions.py:523-609) has no split-KV form. */
+int spyre_paged_decode_attn_split_f16(const void* q, const void* k_cache, const void* v_cache,
+                                      const int32_t* block_table, int64_t bt_stride,
+                                      const int32_t* context_lens, void* workspace,
+                                      size_t workspace_bytes, int B, int Hq, int Hkv, int D,
+                                      int page_size, int64_t num_pages, int max_context_len,
+                                      int split_tokens, float scale, void* stream);
+int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* workspace,
+                                      size_t workspace_bytes, void* out, float* lse, int B, int Hq,
+                                      int Hkv, int D, int max_context_len, int split_tokens,
+                                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

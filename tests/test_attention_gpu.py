@@ -214,3 +214,50 @@ def test_argument_errors(cuda):
         run(cache, table, lens_t, q, cuda, workspace=torch.empty(4, dtype=torch.uint8, device=cuda))
     with pytest.raises(tsa._lib.SpyreHipError):
         run(cache, table, lens_t, q, cuda, split_tokens=100)
+
+
+def test_two_pass_api_equals_single_call_bitexact(cuda):
+    """paged_decode_split + paged_decode_merge == paged_decode_attention."""
+    import torch_spyre_amd as tsa
+
+    lens = [700, 64, 1999]
+    cache, table, lens_t, q = make_case(cuda, 3, 32, 8, 128, lens, SEED + 41)
+    t, l = table.to(cuda), lens_t.to(cuda)
+    ws = torch.empty(tsa.workspace_bytes(3, 32, 8, 128, max(lens), 256), dtype=torch.uint8, device=cuda)
+    one, lse1 = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=256,
+                                           max_context_len=max(lens), return_lse=True)
+    tsa.paged_decode_split(q, cache.k, cache.v, t, l, ws, split_tokens=256, max_context_len=max(lens))
+    two = torch.empty_like(q)
+    lse2 = torch.empty((3, 32), dtype=torch.float32, device=cuda)
+    tsa.paged_decode_merge(l, ws, two, 8, max(lens), split_tokens=256, lse=lse2)
+    assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(lse1, lse2)
+
+
+def test_prepared_call_matches(cuda):
+    """PagedDecode (validated once, launched repeatedly) == paged_decode_attention."""
+    import torch_spyre_amd as tsa
+
+    lens = [300, 1200]
+    cache, table, lens_t, q = make_case(cuda, 2, 16, 4, 128, lens, SEED + 51)
+    t, l = table.to(cuda), lens_t.to(cuda)
+    want = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, max_context_len=max(lens))
+    call = tsa.PagedDecode(q, cache.k, cache.v, t, l, max_context_len=max(lens))
+    for _ in range(3):
+        got = call()
+    assert torch.equal(want.view(torch.int16), got.view(torch.int16))
+
+
+def test_large_batch_grid_mode(cuda):
+    """Batches over 1024 sequences take the grid-mode split kernel; sampled
+    rows (including empty and one-token contexts) against the oracle."""
+    g = torch.Generator().manual_seed(SEED + 61)
+    B = 1100
+    lens = torch.randint(0, 300, (B,), generator=g).tolist()
+    lens[0], lens[1], lens[2] = 0, 1, 299
+    cache, table, lens_t, q = make_case(cuda, B, 8, 2, 64, lens, SEED + 62)
+    out = run(cache, table, lens_t, q, cuda, split_tokens=128)
+    rows = [1, 2, 5, 500, 777, B - 1]
+    rows = [r for r in rows if lens[r] > 0]
+    assert_close(out[rows], oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(64)))
+    assert torch.count_nonzero(out[0]) == 0

@@ -32,11 +32,14 @@ from .relayout import (  # noqa: E402
     transpose_restick_layout,
 )
 from .attention import (  # noqa: E402
+    PagedDecode,
     PagedKVCache,
     dense_to_pages,
     k_page_layout,
     kv_append,
     paged_decode_attention,
+    paged_decode_merge,
+    paged_decode_split,
     sdpa_decode,
     v_page_layout,
     workspace_bytes,
@@ -47,6 +50,7 @@ __all__ = [
     "DataFormats", "ElementArrangement", "SpyreTensorLayout", "dma_plan", "get_device_dtype",
     "restick_plan", "copy_tensor", "device_tensor_layout", "from_device_layout", "overwrite",
     "restickify", "spyre_empty_with_layout", "to_device_layout", "transpose_restick_layout",
-    "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
+    "PagedDecode", "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
+    "paged_decode_merge", "paged_decode_split",
     "sdpa_decode", "v_page_layout", "workspace_bytes",
 ]

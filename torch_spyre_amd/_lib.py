@@ -1,7 +1,7 @@
 """ctypes binding of libspyre_hip.so (the C ABI declared in include/spyre_hip.h).
 
 There is no fallback: if the library is not built, importing the package's
-GPU entry points raises.  Build it with ``python -m torch_spyre_amd.build``
+GPU entry points raises.  Build it with ``python torch_spyre_amd/build.py``
 (or ``__graft_entry__.build()``).
 """
 
@@ -12,7 +12,7 @@ import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint64, c_void_p
 
 LIB_NAME = "libspyre_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+LIB_PATH = os.environ.get("SPYRE_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 SPYRE_OK = 0
 SPYRE_EINVAL = -1
@@ -71,6 +71,11 @@ SIGNATURES = {
                                             c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int,
                                             c_int, c_int, c_int, c_int64, c_int, c_int, c_float,
                                             c_void_p]),
+    "spyre_paged_decode_attn_split_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                                  c_void_p, c_size_t, c_int, c_int, c_int, c_int, c_int,
+                                                  c_int64, c_int, c_int, c_float, c_void_p]),
+    "spyre_paged_decode_attn_merge_f16": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_int,
+                                                  c_int, c_int, c_int, c_int, c_int, c_void_p]),
 }
 
 _lib = None
@@ -89,7 +94,7 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(
-                f"{LIB_PATH} is not built; run `python -m torch_spyre_amd.build` first "
+                f"{LIB_PATH} is not built; run `python torch_spyre_amd/build.py` first "
                 "(the package has no CPU fallback)")
         handle = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():

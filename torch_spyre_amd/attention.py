@@ -116,6 +116,44 @@ def workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_context_len: int, spl
     return int(_lib.lib().spyre_paged_decode_attn_workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens))
 
 
+class _DecodeArgs:
+    """Validated arguments shared by the decode entry points."""
+
+    def __init__(self, q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
+                 max_context_len, workspace):
+        _require_cuda(q, "q")
+        if q.dtype != torch.float16 or q.dim() != 3 or not q.is_contiguous():
+            raise ValueError("q must be contiguous float16 [B, Hq, D]")
+        B, Hq, D = q.shape
+        Hkv = k_cache.shape[1]
+        if Hq % Hkv:
+            raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+        self.num_pages = _check_cache(k_cache, v_cache, Hkv, D)
+        if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
+                or block_table.stride(1) != 1 or not block_table.is_cuda:
+            raise ValueError("block_table must be a CUDA int32 [B, W] tensor with unit column stride")
+        if context_lens.dtype != torch.int32 or context_lens.shape != (B,) or not context_lens.is_contiguous() \
+                or not context_lens.is_cuda:
+            raise ValueError("context_lens must be a contiguous CUDA int32 [B] tensor")
+        if max_context_len is None:
+            max_context_len = int(context_lens.max().item()) if B else 0
+        if max_context_len > block_table.shape[1] * PAGE:
+            raise ValueError(f"max_context_len {max_context_len} exceeds the block table's "
+                             f"{block_table.shape[1]} pages")
+        self.scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+        need = workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens)
+        if workspace is None:
+            workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+        elif workspace.numel() * workspace.element_size() < need:
+            raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, need {need}")
+        self.q, self.k, self.v, self.table, self.lens = q, k_cache, v_cache, block_table, context_lens
+        self.B, self.Hq, self.Hkv, self.D = B, Hq, Hkv, D
+        self.max_ctx, self.split = max_context_len, split_tokens
+        self.ws = workspace
+        self.ws_bytes = workspace.numel() * workspace.element_size()
+        self.stream = _stream_ptr(q.device)
+
+
 def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            block_table: torch.Tensor, context_lens: torch.Tensor,
                            scale: Optional[float] = None, split_tokens: int = 512,
@@ -127,42 +165,97 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
 
     q [B, Hq, D] fp16; caches as PagedKVCache; block_table int32 [B, W];
     context_lens int32 [B].  ``max_context_len`` bounds every context (if
-    omitted it is read from context_lens, which synchronises)."""
-    _require_cuda(q, "q")
-    if q.dtype != torch.float16 or q.dim() != 3 or not q.is_contiguous():
-        raise ValueError("q must be contiguous float16 [B, Hq, D]")
-    B, Hq, D = q.shape
-    Hkv = k_cache.shape[1]
-    if Hq % Hkv:
-        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
-    num_pages = _check_cache(k_cache, v_cache, Hkv, D)
-    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
-            or block_table.stride(1) != 1 or not block_table.is_cuda:
-        raise ValueError("block_table must be a CUDA int32 [B, W] tensor with unit column stride")
-    if context_lens.dtype != torch.int32 or context_lens.shape != (B,) or not context_lens.is_contiguous():
-        raise ValueError("context_lens must be contiguous int32 [B]")
-    if max_context_len is None:
-        max_context_len = int(context_lens.max().item()) if B else 0
-    if max_context_len > block_table.shape[1] * PAGE:
-        raise ValueError(f"max_context_len {max_context_len} exceeds the block table's "
-                         f"{block_table.shape[1]} pages")
-    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    need = workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens)
-    if workspace is None:
-        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
-    elif workspace.numel() * workspace.element_size() < need:
-        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, need {need}")
+    omitted it is read from context_lens, which synchronises).  Runs the
+    split pass then the merge pass."""
+    a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
+                    max_context_len, workspace)
     if out is None:
         out = torch.empty_like(q)
-    lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
+    lse = torch.empty((a.B, a.Hq), dtype=torch.float32, device=q.device) if return_lse else None
     rc = _lib.lib().spyre_paged_decode_attn_f16(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
         block_table.stride(0), context_lens.data_ptr(), out.data_ptr(),
-        lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, PAGE, num_pages,
-        max_context_len, split_tokens, scale, _stream_ptr(q.device))
+        lse.data_ptr() if lse is not None else None, a.ws.data_ptr(), a.ws_bytes, a.B, a.Hq, a.Hkv,
+        a.D, PAGE, a.num_pages, a.max_ctx, a.split, a.scale, a.stream)
     _lib.check("spyre_paged_decode_attn_f16", rc)
     return (out, lse) if return_lse else out
+
+
+class PagedDecode:
+    """A validated decode call that can be launched repeatedly.
+
+    Checks shapes, dtypes and the workspace once; each launch then only
+    passes the stored device pointers to the library (the tensors must stay
+    alive and keep their storage).  ``split()`` and ``merge()`` launch the
+    two passes separately; ``__call__`` runs both."""
+
+    def __init__(self, q, k_cache, v_cache, block_table, context_lens, scale=None,
+                 split_tokens: int = 512, max_context_len: Optional[int] = None, workspace=None,
+                 out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+        a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
+                        max_context_len, workspace)
+        self.out = torch.empty_like(q) if out is None else out
+        if self.out.shape != q.shape or self.out.dtype != q.dtype or not self.out.is_contiguous():
+            raise ValueError("out must be contiguous and shaped like q")
+        if lse is not None and (lse.dtype != torch.float32 or lse.shape != (a.B, a.Hq)):
+            raise ValueError("lse must be float32 [B, Hq]")
+        self.lse = lse
+        self._a = a
+        L = _lib.lib()
+        self._split_fn = L.spyre_paged_decode_attn_split_f16
+        self._merge_fn = L.spyre_paged_decode_attn_merge_f16
+        self._split_args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+                            block_table.stride(0), context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes,
+                            a.B, a.Hq, a.Hkv, a.D, PAGE, a.num_pages, a.max_ctx, a.split, a.scale,
+                            a.stream)
+        self._merge_args = (context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes, self.out.data_ptr(),
+                            lse.data_ptr() if lse is not None else None, a.B, a.Hq, a.Hkv, a.D,
+                            a.max_ctx, a.split, a.stream)
+
+    def split(self) -> None:
+        _lib.check("spyre_paged_decode_attn_split_f16", self._split_fn(*self._split_args))
+
+    def merge(self) -> torch.Tensor:
+        _lib.check("spyre_paged_decode_attn_merge_f16", self._merge_fn(*self._merge_args))
+        return self.out
+
+    def __call__(self) -> torch.Tensor:
+        self.split()
+        return self.merge()
+
+
+def paged_decode_split(q, k_cache, v_cache, block_table, context_lens, workspace: torch.Tensor,
+                       scale: Optional[float] = None, split_tokens: int = 512,
+                       max_context_len: Optional[int] = None) -> None:
+    """Pass 1 only: per-split partials into ``workspace``."""
+    a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
+                    max_context_len, workspace)
+    rc = _lib.lib().spyre_paged_decode_attn_split_f16(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+        block_table.stride(0), context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes, a.B, a.Hq,
+        a.Hkv, a.D, PAGE, a.num_pages, a.max_ctx, a.split, a.scale, a.stream)
+    _lib.check("spyre_paged_decode_attn_split_f16", rc)
+
+
+def paged_decode_merge(context_lens: torch.Tensor, workspace: torch.Tensor, out: torch.Tensor,
+                       Hkv: int, max_context_len: int, split_tokens: int = 512,
+                       lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Pass 2 only: combine the partials written by ``paged_decode_split``
+    (same context_lens, max_context_len and split_tokens) into out [B, Hq, D]."""
+    _require_cuda(out, "out")
+    if out.dtype != torch.float16 or out.dim() != 3 or not out.is_contiguous():
+        raise ValueError("out must be contiguous float16 [B, Hq, D]")
+    B, Hq, D = out.shape
+    if context_lens.dtype != torch.int32 or context_lens.shape != (B,) or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be contiguous int32 [B]")
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, Hq) or not lse.is_contiguous()):
+        raise ValueError("lse must be contiguous float32 [B, Hq]")
+    rc = _lib.lib().spyre_paged_decode_attn_merge_f16(
+        context_lens.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        out.data_ptr(), lse.data_ptr() if lse is not None else None, B, Hq, Hkv, D,
+        max_context_len, split_tokens, _stream_ptr(out.device))
+    _lib.check("spyre_paged_decode_attn_merge_f16", rc)
+    return out
 
 
 def dense_to_pages(k: torch.Tensor, v: torch.Tensor) -> tuple[PagedKVCache, torch.Tensor]:

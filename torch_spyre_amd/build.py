@@ -1,6 +1,8 @@
 """Builds libspyre_hip.so in-tree for gfx950 with hipcc.
 
-    python -m torch_spyre_amd.build
+    python torch_spyre_amd/build.py
+
+(Run it by path: importing the package loads the library this builds.)
 
 Objects go to torch_spyre_amd/_build/ (compiled in parallel), the shared
 library to torch_spyre_amd/libspyre_hip.so.
@@ -26,11 +28,11 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall"]
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+def _compile(src: str, build_dir: str = BUILD, defines=()) -> str:
+    obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
     path = os.path.join(CSRC, src)
     if src.endswith(".hip"):
-        cmd = [HIPCC, *COMMON, *DEVICE, "-c", path, "-o", obj]
+        cmd = [HIPCC, *COMMON, *DEVICE, *[f"-D{d}" for d in defines], "-c", path, "-o", obj]
     else:
         cmd = [HIPCC, *COMMON, "-x", "c++", "-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -39,19 +41,21 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build(verbose: bool = False, out: str = OUT, build_dir: str = BUILD, defines=()) -> str:
+    """Compiles every source and links ``out``; ``defines`` are extra -D
+    macros for the device sources (kernel variants)."""
+    os.makedirs(build_dir, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = OUT + ".tmp"
+        objs = list(ex.map(lambda f: _compile(f, build_dir, defines), SOURCES))
+    tmp = out + ".tmp"
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT}")
-    return OUT
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":

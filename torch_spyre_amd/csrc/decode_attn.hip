@@ -8,29 +8,32 @@
 // Cache layout (64-token pages, one page = 16 KiB per KV head and tensor):
 //   K  [num_pages, Hkv, D/64, 64 tok, 64]   sticks along D    (QK^T reduces over D)
 //   V  [num_pages, Hkv, D, 64 tok]          sticks along tokens (PV reduces over tokens)
-// so that the reduction dim of both products is contiguous and every MFMA
-// operand is one 16-byte load straight from HBM into VGPRs.
+// so that the reduction dim of both products is contiguous: every MFMA
+// operand is built from whole 128-byte sticks loaded straight into VGPRs.
 //
-// Pass 1 (decode_split_kernel): one workgroup of 4 wavefronts per
-// (sequence, KV head, split of `split_pages` pages).  The pages of a split
-// rotate through the 4 wavefronts (the KV carousel); each wavefront streams a
-// whole page per iteration:
-//   S^T[tok, head] = K[tok, :] Q^T[:, head]   4 x 4 MFMA 16x16x32 (M = 16 tokens)
+// Pass 1 (decode_split_list_kernel; decode_split_kernel for batches over
+// kMaxListSeqs): one wavefront per work item (sequence, KV head, split of
+// `split_pages` pages).  The split's pages rotate through the wavefront's
+// operand registers -- the KV carousel: page i+1's K loads are issued as
+// soon as page i's QK MFMAs have consumed their registers, its V loads as
+// soon as PV has -- and each page is
+//   S^T[tok, head] = K[tok, :] Q^T[:, head]   4 x D/32 MFMA 16x16x32 (M = 16 tokens)
 //   online softmax in fp32 (exp2 domain), row max across the 4 lane groups
 //   of a head by lane shuffles;
 //   O^T[d, head] += V^T[d, tok] P^T[tok, head]   D/16 x 2 MFMA 16x16x32
 // The q heads of one KV head (g of them, padded to the MFMA's 16 columns)
 // form the dense N dimension, so K and V are read once for all g heads.
 // The token order of the QK rows is permuted so that each lane's P values
-// are exactly the 8 consecutive tokens the PV B operand needs (no shuffles).
-// The 4 wavefronts' (m, l, O) are merged through LDS and the split's partial
-// is written to the workspace.
+// are exactly the 8 consecutive tokens the PV B operand needs.  The split's
+// partial (unnormalised O, running max, row sum) goes from registers to the
+// workspace; no LDS and no barrier is involved.
 //
 // Pass 2 (decode_merge_kernel): per (sequence, q head) combine the splits'
 // partials -- the split-KV merge -- and write fp16 out (+ optional LSE).
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "spyre_common.h"
@@ -60,9 +63,21 @@ struct SplitArgs {
   const int32_t* ctx_lens;
   float* ws;
   int64_t num_pages;
-  int Hq, Hkv, g, max_splits, split_pages, max_ctx;
+  int B, Hq, Hkv, g, max_splits, split_pages, max_ctx;
   float scale_log2;
 };
+
+// Work-list mode handles batches up to this many sequences (their split
+// counts are prefix-summed in LDS); larger batches use grid mode.
+#ifndef SPYRE_DECODE_LIST_MAX
+#define SPYRE_DECODE_LIST_MAX 1024
+#endif
+constexpr int kMaxListSeqs = SPYRE_DECODE_LIST_MAX;
+
+// Wavefronts per SIMD the split kernels are compiled for: two pages of
+// operands (the one being computed and the next one in flight) take the
+// 256 VGPRs that two wavefronts per SIMD leave each.
+constexpr int kWavesPerSimd = 2;
 
 // ---- Operand loads: whole cache lines, then a lane shuffle --------------
 //
@@ -103,19 +118,47 @@ __device__ __forceinline__ int qk_token(int jh, int i) {
   return 32 * (jh >> 1) + 8 * (i >> 2) + 4 * (jh & 1) + (i & 3);
 }
 
+// Pages are read with buffer loads: a resource (base, size) per page in
+// SGPRs, a 32-bit per-lane offset in a VGPR and the load-invariant part of
+// the offset in an SGPR / immediate.  This keeps address registers to four
+// VGPRs per wavefront, and the hardware clamps every access to the page.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit format
+constexpr int kLoadNT = 2;              // non-temporal: K/V are streamed once
+
+__device__ __forceinline__ Rsrc page_rsrc(const _Float16* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), 0, bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ f16x8 bload(Rsrc r, int voff, int soff) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT));
+}
+
+// Per-lane byte offsets of the raw loads (see the X / Y scheme above).
+struct LoadOffsets {
+  int kx, ky, vx, vy;
+  __device__ __forceinline__ explicit LoadOffsets(int lane) {
+    const int r = lane & 7, cx = chunk_x(lane), cy = chunk_y(lane);
+    const int tx = 8 * (r >> 2) + (r & 3);  // qk_token(0, r); block jh adds 32j + 4h
+    kx = (tx * 64 + cx * 8) * 2;
+    ky = ((tx + 16) * 64 + cy * 8) * 2;     // row 8 + r is token tx + 16
+    vx = (r * kPage + cx * 8) * 2;
+    vy = ((8 + r) * kPage + cy * 8) * 2;
+  }
+};
+
 // Raw K loads of one page: for block jh and stick tile t, X -> ka[jh][2t],
 // Y -> ka[jh][2t+1] (operands after shuffle_pair: d = 32 ds + 8 (l>>4)).
 template <int D>
-__device__ __forceinline__ void load_k(f16x8 (&ka)[4][D / 32], const _Float16* kp, int lane) {
-  const int cx = chunk_x(lane), cy = chunk_y(lane), r = lane & 7;
+__device__ __forceinline__ void load_k(f16x8 (&ka)[4][D / 32], Rsrc kr, const LoadOffsets& lo) {
 #pragma unroll
   for (int jh = 0; jh < 4; ++jh) {
-    const int tx = qk_token(jh, r), ty = qk_token(jh, 8 + r);
 #pragma unroll
     for (int t = 0; t < D / 64; ++t) {
-      const _Float16* tile = kp + t * (kPage * 64);
-      ka[jh][2 * t] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(tile + tx * 64 + cx * 8));
-      ka[jh][2 * t + 1] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(tile + ty * 64 + cy * 8));
+      const int so = ((32 * (jh >> 1) + 4 * (jh & 1)) * 64 + t * (kPage * 64)) * 2;
+      ka[jh][2 * t] = bload(kr, lo.kx, so);
+      ka[jh][2 * t + 1] = bload(kr, lo.ky, so);
     }
   }
 }
@@ -124,32 +167,33 @@ __device__ __forceinline__ void load_k(f16x8 (&ka)[4][D / 32], const _Float16* k
 // va[db][0], Y (rows 16db + 8..15) -> va[db][1]; after shuffle_pair
 // va[db][j] is the operand for tokens 32j + 8 (l>>4) .. +8.
 template <int D>
-__device__ __forceinline__ void load_v(f16x8 (&va)[D / 16][2], const _Float16* vp, int lane) {
-  const int cx = chunk_x(lane), cy = chunk_y(lane), r = lane & 7;
+__device__ __forceinline__ void load_v(f16x8 (&va)[D / 16][2], Rsrc vr, const LoadOffsets& lo) {
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
-    va[db][0] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vp + (16 * db + r) * kPage + cx * 8));
-    va[db][1] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vp + (16 * db + 8 + r) * kPage + cy * 8));
+    const int so = 16 * db * kPage * 2;
+    va[db][0] = bload(vr, lo.vx, so);
+    va[db][1] = bload(vr, lo.vy, so);
   }
 }
 
+// One work item -- split s of sequence b, KV head kvh -- streamed by one
+// wavefront: its pages rotate through the operand registers (the next page's
+// K loads are issued as soon as this page's QK MFMAs have consumed theirs),
+// and the split's partial (unnormalised O, running max m, row sum l) goes
+// straight from registers to the workspace.  No LDS, no barriers.
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(SplitArgs a) {
+__device__ __forceinline__ void process_item(const SplitArgs& a, int b, int s, int kvh, int lane) {
   constexpr int DS = D / 32;  // QK K-steps
   constexpr int DB = D / 16;  // PV output blocks
-  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int ctx = min(max(a.ctx_lens[b], 0), a.max_ctx);
   const int n_pages = (ctx + kPage - 1) / kPage;
   const int p0 = s * a.split_pages;
   if (p0 >= n_pages) return;
-  const int p1 = min(p0 + a.split_pages, n_pages);
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int n_it = min(a.split_pages, n_pages - p0);
   const int col = lane & 15, grp = lane >> 4;
-  // This wavefront's pages: p0 + wave + kWaves * it, it < n_it.
-  const int n_it = (p1 - p0 - wave + kWaves - 1) / kWaves;
-  const int32_t* trow = a.block_table + static_cast<int64_t>(b) * a.bt_stride + p0 + wave;
-  // One lane per page: the page ids of the next 64 iterations.
-  int ids = lane < n_it ? trow[kWaves * lane] : 0;
+  const int32_t* trow = a.block_table + static_cast<int64_t>(b) * a.bt_stride + p0;
+  // One lane per page: the page ids of the next 64 pages.
+  int ids = lane < n_it ? trow[lane] : 0;
 
   // Q^T operand: lane = (head col, d group grp); padded heads are zero.
   f16x8 qb[DS];
@@ -171,138 +215,176 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(SplitArgs a) 
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (n_it > 0) {
-    // Page it's K/V base pointers (page id broadcast from lane it % 64).
-    auto locate = [&](int it, const _Float16*& kp, const _Float16*& vp) {
-      int64_t phys = __builtin_amdgcn_readlane(ids, it & 63);
-      const bool bad = phys < 0 || phys >= a.num_pages;
-      poisoned |= bad;
-      if (bad) phys = 0;  // stay in bounds; the result is poisoned below
-      kp = a.k + phys * page_elems + kvh * head_elems;
-      vp = a.v + phys * page_elems + kvh * head_elems;
-    };
-    const _Float16 *kp, *vp;
-    locate(0, kp, vp);
-    f16x8 ka[4][DS];
-    f16x8 va[DB][2];
-    load_k<D>(ka, kp, lane);
-    load_v<D>(va, vp, lane);
+  // Page it's K/V resources (page id broadcast from lane it % 64).
+  const int head_bytes = static_cast<int>(head_elems * 2);
+  auto locate = [&](int it, Rsrc& kr, Rsrc& vr) {
+    int64_t phys = __builtin_amdgcn_readlane(ids, it & 63);
+    const bool bad = phys < 0 || phys >= a.num_pages;
+    poisoned |= bad;
+    if (bad) phys = 0;  // stay in bounds; the result is poisoned below
+    kr = page_rsrc(a.k + phys * page_elems + kvh * head_elems, head_bytes);
+    vr = page_rsrc(a.v + phys * page_elems + kvh * head_elems, head_bytes);
+  };
+  const LoadOffsets lo(lane);
+  Rsrc kr, vr;
+  locate(0, kr, vr);
+  f16x8 ka[4][DS];
+  f16x8 va[DB][2];
+  load_k<D>(ka, kr, lo);
+  load_v<D>(va, vr, lo);
 
-    for (int it = 0; it < n_it; ++it) {
-      const int valid = min(kPage, ctx - (p0 + wave + kWaves * it) * kPage);
-      const bool bit3 = (lane & 8) != 0;
+  for (int it = 0; it < n_it; ++it) {
+    const int valid = min(kPage, ctx - (p0 + it) * kPage);
+    const bool bit3 = (lane & 8) != 0;
 #pragma unroll
-      for (int jh = 0; jh < 4; ++jh)
+    for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
-        for (int t = 0; t < DS / 2; ++t) shuffle_pair(ka[jh][2 * t], ka[jh][2 * t + 1], bit3);
-      f32x4 sc[4];
+      for (int t = 0; t < DS / 2; ++t) shuffle_pair(ka[jh][2 * t], ka[jh][2 * t + 1], bit3);
+    f32x4 sc[4];
 #pragma unroll
-      for (int jh = 0; jh < 4; ++jh) {
-        sc[jh] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int jh = 0; jh < 4; ++jh) {
+      sc[jh] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds)
-          sc[jh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[ds], sc[jh], 0, 0, 0);
+      for (int ds = 0; ds < DS; ++ds)
+        sc[jh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[ds], sc[jh], 0, 0, 0);
+    }
+    // The K registers are consumed: start the next page's K loads now, so
+    // they are in flight during this page's softmax and PV.
+    const bool more = it + 1 < n_it;
+    if (more) {
+      if (((it + 1) & 63) == 0) {
+        const int nx = it + 1 + lane;
+        ids = nx < n_it ? trow[nx] : 0;
       }
-      // The K registers are consumed: start the next page's K loads now, so
-      // they are in flight during this page's softmax and PV.
-      const bool more = it + 1 < n_it;
-      if (more) {
-        if (((it + 1) & 63) == 0) {
-          const int nx = it + 1 + lane;
-          ids = nx < n_it ? trow[kWaves * nx] : 0;
-        }
-        locate(it + 1, kp, vp);
-        load_k<D>(ka, kp, lane);
-      }
+      locate(it + 1, kr, vr);
+      load_k<D>(ka, kr, lo);
+    }
 
-      // This lane holds head col's scores for tokens 32j + 8grp + 4h + v.
-      float mx = -INFINITY;
+    // This lane holds head col's scores for tokens 32j + 8grp + 4h + v.
+    float mx = -INFINITY;
 #pragma unroll
-      for (int jh = 0; jh < 4; ++jh)
+    for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int t = 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
-          const float x = t < valid ? sc[jh][v] * a.scale_log2 : -INFINITY;
-          sc[jh][v] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, wave_xor(mx, 16));
-      mx = fmaxf(mx, wave_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
-      float psum = 0.f;
-      f16x8 pb[2];
-#pragma unroll
-      for (int jh = 0; jh < 4; ++jh)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float pv = fast_exp2(sc[jh][v] - m_new);
-          psum += pv;
-          pb[jh >> 1][(jh & 1) * 4 + v] = static_cast<_Float16>(pv);
-        }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) o[db] *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) shuffle_pair(va[db][0], va[db][1], bit3);
-      if (valid < kPage) {
-        // Tokens past the context may hold any bits (even NaN); zero them so
-        // that 0 * V stays 0 in the PV product.
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if (32 * j + 8 * grp + e >= valid) va[db][j][e] = static_cast<_Float16>(0.f);
+      for (int v = 0; v < 4; ++v) {
+        const int t = 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
+        const float x = t < valid ? sc[jh][v] * a.scale_log2 : -INFINITY;
+        sc[jh][v] = x;
+        mx = fmaxf(mx, x);
       }
+    mx = fmaxf(mx, wave_xor(mx, 16));
+    mx = fmaxf(mx, wave_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    float psum = 0.f;
+    f16x8 pb[2];
+#pragma unroll
+    for (int jh = 0; jh < 4; ++jh)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float pv = fast_exp2(sc[jh][v] - m_new);
+        psum += pv;
+        pb[jh >> 1][(jh & 1) * 4 + v] = static_cast<_Float16>(pv);
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] *= alpha;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) shuffle_pair(va[db][0], va[db][1], bit3);
+    if (valid < kPage) {
+      // Tokens past the context may hold any bits (even NaN); zero them so
+      // that 0 * V stays 0 in the PV product.
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
-      if (more) load_v<D>(va, vp, lane);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (32 * j + 8 * grp + e >= valid) va[db][j][e] = static_cast<_Float16>(0.f);
     }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
+    if (more) load_v<D>(va, vr, lo);
   }
   if (poisoned) l_run = NAN;  // propagates to the merged output: NaN, not a fault
-
   l_run += wave_xor(l_run, 16);
   l_run += wave_xor(l_run, 32);
 
-  __shared__ float sm_m[kWaves][kCols], sm_l[kWaves][kCols];
-  __shared__ float sm_o[kWaves][kCols][D];
-  if (grp == 0) {
-    sm_m[wave][col] = m_run;
-    sm_l[wave][col] = l_run;
+  // Partial of this split: lane (head col, group grp) holds
+  // O^T[d = 16db + 4grp + v][col] -- 16 contiguous bytes per db.
+  if (col < a.g) {
+    const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits + s;
+    float* wo = a.ws + (slot * a.g + col) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(wo + 16 * db + 4 * grp) = o[db];
+    if (grp == 0) {
+      float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + (slot * a.g + col) * 2;
+      wm[0] = m_run;
+      wm[1] = l_run;
+    }
   }
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) sm_o[wave][col][16 * db + 4 * grp + v] = o[db][v];
-  __syncthreads();
+}
 
-  const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits + s;
-  float* wo = a.ws + slot * a.g * D;
-  float* wm = a.ws + static_cast<int64_t>(gridDim.z) * a.Hkv * a.max_splits * a.g * D + slot * a.g * 2;
-  for (int idx = threadIdx.x; idx < a.g * D; idx += kThreads) {
-    const int h = idx / D, d = idx % D;
-    float M = sm_m[0][h];
+// Grid mode: blockIdx = (group of kWaves splits, KV head, sequence); wavefront
+// w takes split kWaves * blockIdx.x + w.  Splits past a sequence's context
+// return at once.
+template <int D>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_kernel(SplitArgs a) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  process_item<D>(a, blockIdx.z, kWaves * blockIdx.x + wave, blockIdx.y, lane);
+}
+
+// Work-list mode: the items (sequence, split, KV head) that exist are
+// numbered densely -- each workgroup prefix-sums the per-sequence split
+// counts in LDS -- and wavefront w of workgroup x takes item 4x + w.  Real
+// items come first, so no workgroup is spent on a split past a sequence's
+// end until all real ones have been dispatched; ragged batches stay
+// balanced.
+template <int D>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_list_kernel(SplitArgs a) {
+  __shared__ int s_pre[kMaxListSeqs > 0 ? kMaxListSeqs + 1 : 1];
+  const int split_tokens = a.split_pages * kPage;
+  for (int i = threadIdx.x; i < a.B; i += kThreads) {
+    const int c = min(max(a.ctx_lens[i], 0), a.max_ctx);
+    s_pre[i + 1] = (c + split_tokens - 1) / split_tokens;
+  }
+  if (threadIdx.x == 0) s_pre[0] = 0;
+  __syncthreads();
+  if (threadIdx.x < 64) {  // inclusive scan of s_pre[1..B], 64 at a time
+    const int lane = threadIdx.x;
+    int carry = 0;
+    for (int base = 1; base <= a.B; base += 64) {
+      const int i = base + lane;
+      int v = i <= a.B ? s_pre[i] : 0;
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
-    float acc = 0.f, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(sm_m[w][h] - M);  // waves without pages: exp2(-inf) = 0
-      acc += sm_o[w][h][d] * f;
-      L += sm_l[w][h] * f;
-    }
-    wo[h * D + d] = acc;
-    if (d == 0) {
-      wm[2 * h] = M;
-      wm[2 * h + 1] = L;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+      }
+      if (i <= a.B) s_pre[i] = v + carry;
+      carry += __shfl(v, 63, 64);
     }
   }
+  __syncthreads();
+  const int total = s_pre[a.B] * a.Hkv;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  auto run = [&](int item) {
+    // item is wavefront-uniform; readfirstlane keeps it (and all that
+    // derives from it) in scalar registers.
+    item = __builtin_amdgcn_readfirstlane(item);
+    const int bs = item / a.Hkv, kvh = item - bs * a.Hkv;
+    int lo = 0, hi = a.B;  // s_pre[lo] <= bs < s_pre[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (__builtin_amdgcn_readfirstlane(s_pre[mid]) <= bs) lo = mid; else hi = mid;
+    }
+    process_item<D>(a, lo, bs - __builtin_amdgcn_readfirstlane(s_pre[lo]), kvh, lane);
+  };
+  const int item = blockIdx.x * kWaves + wave;
+  if (item < total) run(item);
 }
 
 struct MergeArgs {
@@ -313,34 +395,23 @@ struct MergeArgs {
   int B, Hq, Hkv, g, max_splits, split_tokens, max_ctx;
 };
 
-template <int D>
-__device__ __forceinline__ float block_reduce(float x, bool is_max, float* scratch) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float y = __shfl_xor(x, m, 64);
-    x = is_max ? fmaxf(x, y) : x + y;
-  }
-  const int w = threadIdx.x / 64;
-  if ((threadIdx.x & 63) == 0) scratch[w] = x;
-  __syncthreads();
-  float r = scratch[0];
-#pragma unroll
-  for (int i = 1; i < D / 64; ++i) r = is_max ? fmaxf(r, scratch[i]) : r + scratch[i];
-  __syncthreads();
-  return r;
-}
+// Split-KV merge: one block of D threads per (q head, sequence).  All loads
+// of a chunk of kMergeChunk splits (m, l and the thread's O column) are
+// issued together before any of them is used, so a chunk costs one memory
+// latency; splits past the sequence's count are read (in bounds: the
+// workspace holds max_splits) and discarded by selects, never multiplied.
+constexpr int kMergeChunk = 16;
 
-// Split-KV merge: one block of D threads per (q head, sequence).  The splits'
-// weights exp2(m_s - M) are computed once per chunk of D splits into LDS,
-// then each thread (one output feature) sums its column with 8-way unrolled
-// independent loads.
 template <int D>
 __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
-  __shared__ float s_w[D];
-  __shared__ float s_red[D / 64];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int kvh = h / a.g, hh = h % a.g;
   const int ctx_raw = a.ctx_lens[b];
+  const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits;
+  const float* wo = a.ws + slot0 * a.g * D + hh * D + d;
+  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + slot0 * a.g * 2 + hh * 2;
+  const int64_t so = static_cast<int64_t>(a.g) * D;  // split stride of wo
+  const int sm = 2 * a.g;                              // split stride of wm
   const int ctx = min(max(ctx_raw, 0), a.max_ctx);
   const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
   _Float16* o = a.out + (static_cast<int64_t>(b) * a.Hq + h) * D;
@@ -349,43 +420,35 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
     if (a.lse && d == 0) a.lse[static_cast<int64_t>(b) * a.Hq + h] = -INFINITY;
     return;
   }
-  const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits;
-  const float* wo = a.ws + slot0 * a.g * D + hh * D + d;
-  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + slot0 * a.g * 2 + hh * 2;
-  const int64_t so = static_cast<int64_t>(a.g) * D;  // split stride of wo
-  const int sm = 2 * a.g;                              // split stride of wm
-
-  float mx = -INFINITY;
-  for (int s = d; s < ns; s += D) mx = fmaxf(mx, wm[s * sm]);
-  const float M = block_reduce<D>(mx, true, s_red);
-
-  float acc = 0.f, lpart = 0.f;
-  for (int c = 0; c < ns; c += D) {
-    const int s = c + d;
-    float w = 0.f;
-    if (s < ns) {
-      w = fast_exp2(wm[s * sm] - M);
-      lpart += wm[s * sm + 1] * w;
-    }
-    s_w[d] = w;
-    __syncthreads();
-    const int n = min(D, ns - c);
-    const float* col = wo + c * so;
-    int j = 0;
-    for (; j + 8 <= n; j += 8) {
-      float x[8];
+  // Running (M, L, acc) over chunks, rescaled like the online softmax.
+  float M = -INFINITY, L = 0.f, acc = 0.f;
+  for (int c = 0; c < ns; c += kMergeChunk) {
+    float m[kMergeChunk], l[kMergeChunk], x[kMergeChunk];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = col[(j + u) * so];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc += x[u] * s_w[j + u];
+    for (int u = 0; u < kMergeChunk; ++u) {
+      const int s = min(c + u, a.max_splits - 1);
+      m[u] = wm[s * sm];
+      l[u] = wm[s * sm + 1];
+      x[u] = wo[s * so];
     }
-    for (; j < n; ++j) acc += col[j * so] * s_w[j];
-    __syncthreads();
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u)
+      if (c + u < ns) mc = fmaxf(mc, m[u]);
+    const float r = fast_exp2(M - mc);  // first chunk: exp2(-inf) = 0
+    L *= r;
+    acc *= r;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u) {
+      const float w = fast_exp2(m[u] - mc);
+      L += c + u < ns ? l[u] * w : 0.f;
+      acc += c + u < ns ? x[u] * w : 0.f;
+    }
+    M = mc;
   }
-  const float L = block_reduce<D>(lpart, false, s_red);
-  float r = acc / L;
-  if (ctx_raw > a.max_ctx) r = NAN;  // caller broke the max_context_len contract
-  o[d] = static_cast<_Float16>(r);
+  float res = acc / L;
+  if (ctx_raw > a.max_ctx) res = NAN;  // caller broke the max_context_len contract
+  o[d] = static_cast<_Float16>(res);
   if (a.lse && d == 0) a.lse[static_cast<int64_t>(b) * a.Hq + h] = (M + log2f(L)) * kLn2;
 }
 
@@ -403,16 +466,25 @@ extern "C" size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv
   return static_cast<size_t>(B) * Hkv * ns * g * (D + 2) * sizeof(float);
 }
 
-extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* v_cache,
-                                           const int32_t* block_table, int64_t bt_stride,
-                                           const int32_t* context_lens, void* out, float* lse,
-                                           void* workspace, size_t workspace_bytes, int B, int Hq,
-                                           int Hkv, int D, int page_size, int64_t num_pages,
-                                           int max_context_len, int split_tokens, float scale,
-                                           void* stream) {
-  spyre_hip::clear_error();
-  SPYRE_REQUIRE(q && k_cache && v_cache && block_table && context_lens && out && workspace,
-                SPYRE_EINVAL, "null pointer argument");
+namespace {
+
+struct Plan {
+  SplitArgs sa;
+  MergeArgs ma;
+  dim3 g1, g2;
+  int D;
+  bool list;
+};
+
+int plan_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+              int64_t bt_stride, const int32_t* context_lens, void* out, float* lse, void* workspace,
+              size_t workspace_bytes, int B, int Hq, int Hkv, int D, int page_size,
+              int64_t num_pages, int max_context_len, int split_tokens, float scale, bool need_inputs,
+              bool need_out, Plan& p) {
+  SPYRE_REQUIRE(context_lens && workspace, SPYRE_EINVAL, "null pointer argument");
+  SPYRE_REQUIRE(!need_inputs || (q && k_cache && v_cache && block_table), SPYRE_EINVAL,
+                "null pointer argument");
+  SPYRE_REQUIRE(!need_out || out, SPYRE_EINVAL, "null output pointer");
   SPYRE_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, SPYRE_EINVAL,
                 "bad head counts B=%d Hq=%d Hkv=%d", B, Hq, Hkv);
   const int g = Hq / Hkv;
@@ -421,9 +493,10 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
   SPYRE_REQUIRE(page_size == kPage, SPYRE_EUNSUPPORTED, "page_size %d != %d", page_size, kPage);
   SPYRE_REQUIRE(split_tokens > 0 && split_tokens % kPage == 0, SPYRE_EINVAL,
                 "split_tokens %d must be a positive multiple of %d", split_tokens, kPage);
-  SPYRE_REQUIRE(max_context_len >= 0 && num_pages > 0 && bt_stride >= 0, SPYRE_EINVAL,
-                "bad max_context_len / num_pages / bt_stride");
-  SPYRE_REQUIRE(bt_stride * kPage >= max_context_len || B == 1, SPYRE_EINVAL,
+  SPYRE_REQUIRE(max_context_len >= 0 && bt_stride >= 0, SPYRE_EINVAL,
+                "bad max_context_len / bt_stride");
+  SPYRE_REQUIRE(!need_inputs || num_pages > 0, SPYRE_EINVAL, "bad num_pages");
+  SPYRE_REQUIRE(!need_inputs || B == 1 || bt_stride * kPage >= max_context_len, SPYRE_EINVAL,
                 "block table rows (%lld pages) shorter than max_context_len %d",
                 static_cast<long long>(bt_stride), max_context_len);
   const size_t need =
@@ -431,24 +504,93 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
   SPYRE_REQUIRE(workspace_bytes >= need, SPYRE_ENOSPC, "workspace %zu < %zu bytes",
                 workspace_bytes, need);
   const int max_splits = static_cast<int>(splits_for(max_context_len, split_tokens));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-
-  SplitArgs sa{static_cast<const _Float16*>(q), static_cast<const _Float16*>(k_cache),
-               static_cast<const _Float16*>(v_cache), block_table, bt_stride, context_lens,
-               static_cast<float*>(workspace), num_pages, Hq, Hkv, g, max_splits,
-               split_tokens / kPage, max_context_len, scale * kLog2e};
-  MergeArgs ma{static_cast<const float*>(workspace), context_lens, static_cast<_Float16*>(out),
-               lse, B, Hq, Hkv, g, max_splits, split_tokens, max_context_len};
-  const dim3 g1(max_splits, Hkv, B), g2(Hq, B);
-  if (D == 128) {
-    decode_split_kernel<128><<<g1, kThreads, 0, st>>>(sa);
-    decode_merge_kernel<128><<<g2, 128, 0, st>>>(ma);
+  p.sa = SplitArgs{static_cast<const _Float16*>(q), static_cast<const _Float16*>(k_cache),
+                   static_cast<const _Float16*>(v_cache), block_table, bt_stride, context_lens,
+                   static_cast<float*>(workspace), num_pages, B, Hq, Hkv, g, max_splits,
+                   split_tokens / kPage, max_context_len, scale * kLog2e};
+  p.ma = MergeArgs{static_cast<const float*>(workspace), context_lens, static_cast<_Float16*>(out),
+                   lse, B, Hq, Hkv, g, max_splits, split_tokens, max_context_len};
+  p.D = D;
+  p.list = B <= kMaxListSeqs;
+  if (p.list) {
+    // Upper bound on the items; those past the real count are numbered last
+    // and exit at once.
+    const int64_t wgs = (static_cast<int64_t>(B) * Hkv * max_splits + kWaves - 1) / kWaves;
+    p.g1 = dim3(static_cast<unsigned>(std::max<int64_t>(1, wgs)));
   } else {
-    decode_split_kernel<64><<<g1, kThreads, 0, st>>>(sa);
-    decode_merge_kernel<64><<<g2, 64, 0, st>>>(ma);
+    p.g1 = dim3((max_splits + kWaves - 1) / kWaves, Hkv, B);
   }
-  const hipError_t e = hipGetLastError();
-  SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "decode attention launch failed: %s",
-                hipGetErrorString(e));
+  p.g2 = dim3(Hq, B);
   return SPYRE_OK;
+}
+
+int launch_split(const Plan& p, hipStream_t st) {
+  if (p.list && p.D == 128)
+    decode_split_list_kernel<128><<<p.g1, kThreads, 0, st>>>(p.sa);
+  else if (p.list)
+    decode_split_list_kernel<64><<<p.g1, kThreads, 0, st>>>(p.sa);
+  else if (p.D == 128)
+    decode_split_kernel<128><<<p.g1, kThreads, 0, st>>>(p.sa);
+  else
+    decode_split_kernel<64><<<p.g1, kThreads, 0, st>>>(p.sa);
+  const hipError_t e = hipGetLastError();
+  SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "decode split launch failed: %s", hipGetErrorString(e));
+  return SPYRE_OK;
+}
+
+int launch_merge(const Plan& p, hipStream_t st) {
+  if (p.D == 128)
+    decode_merge_kernel<128><<<p.g2, 128, 0, st>>>(p.ma);
+  else
+    decode_merge_kernel<64><<<p.g2, 64, 0, st>>>(p.ma);
+  const hipError_t e = hipGetLastError();
+  SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "decode merge launch failed: %s", hipGetErrorString(e));
+  return SPYRE_OK;
+}
+
+}  // namespace
+
+extern "C" int spyre_paged_decode_attn_split_f16(
+    const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+    int64_t bt_stride, const int32_t* context_lens, void* workspace, size_t workspace_bytes, int B,
+    int Hq, int Hkv, int D, int page_size, int64_t num_pages, int max_context_len, int split_tokens,
+    float scale, void* stream) {
+  spyre_hip::clear_error();
+  Plan p;
+  int rc = plan_attn(q, k_cache, v_cache, block_table, bt_stride, context_lens, nullptr, nullptr,
+                     workspace, workspace_bytes, B, Hq, Hkv, D, page_size, num_pages,
+                     max_context_len, split_tokens, scale, true, false, p);
+  if (rc != SPYRE_OK) return rc;
+  return launch_split(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* workspace,
+                                                 size_t workspace_bytes, void* out, float* lse, int B,
+                                                 int Hq, int Hkv, int D, int max_context_len,
+                                                 int split_tokens, void* stream) {
+  spyre_hip::clear_error();
+  Plan p;
+  int rc = plan_attn(nullptr, nullptr, nullptr, nullptr, 0, context_lens, out, lse,
+                     const_cast<void*>(workspace), workspace_bytes, B, Hq, Hkv, D, kPage, 1,
+                     max_context_len, split_tokens, 1.f, false, true, p);
+  if (rc != SPYRE_OK) return rc;
+  return launch_merge(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* v_cache,
+                                           const int32_t* block_table, int64_t bt_stride,
+                                           const int32_t* context_lens, void* out, float* lse,
+                                           void* workspace, size_t workspace_bytes, int B, int Hq,
+                                           int Hkv, int D, int page_size, int64_t num_pages,
+                                           int max_context_len, int split_tokens, float scale,
+                                           void* stream) {
+  spyre_hip::clear_error();
+  Plan p;
+  int rc = plan_attn(q, k_cache, v_cache, block_table, bt_stride, context_lens, out, lse, workspace,
+                     workspace_bytes, B, Hq, Hkv, D, page_size, num_pages, max_context_len,
+                     split_tokens, scale, true, true, p);
+  if (rc != SPYRE_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((rc = launch_split(p, st)) != SPYRE_OK) return rc;
+  return launch_merge(p, st);
 }
