@@ -1,0 +1,127 @@
+"""CPU: pin the attention oracle (decomposition restatement, CPU SDPA path,
+page gathering) to torch's SDPA and to closed-form cases."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import layout as OL
+from tests.conftest import SEED
+
+
+def _rand(shape, seed):
+    return torch.randn(shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 8, 8, 512, 64), (2, 32, 8, 100, 128), (3, 16, 2, 7, 64), (1, 4, 1, 1, 128)])
+def test_decomposition_matches_torch_sdpa(B, Hq, Hkv, S, D):
+    q, k, v = _rand((B, Hq, 1, D), 1), _rand((B, Hkv, S, D), 2), _rand((B, Hkv, S, D), 3)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, enable_gqa=Hq != Hkv)
+    got = OA.sdpa_decomposition_fp64(q.numpy(), k.numpy(), v.numpy())
+    assert np.allclose(got, ref.numpy(), atol=1e-12, rtol=1e-10)
+    fp32 = OA.sdpa_cpu_fp32(q, k, v)
+    assert np.allclose(fp32.numpy(), got, atol=1e-5, rtol=1e-4)
+
+
+def test_scale_is_applied_once():
+    """sqrt(scale) on q and on k equals scale on the scores; a scale applied
+    to q only would not match."""
+    q, k, v = _rand((1, 2, 1, 64), 4), _rand((1, 2, 9, 64), 5), _rand((1, 2, 9, 64), 6)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=0.3)
+    assert np.allclose(OA.sdpa_decomposition_fp64(q, k, v, 0.3), ref.numpy(), atol=1e-12)
+    wrong = torch.nn.functional.scaled_dot_product_attention(q * math.sqrt(0.3), k, v, scale=1.0)
+    assert not np.allclose(wrong.numpy(), ref.numpy(), atol=1e-3)
+
+
+def test_single_key_returns_its_value():
+    q, k, v = _rand((2, 4, 1, 64), 7), _rand((2, 2, 1, 64), 8), _rand((2, 2, 1, 64), 9)
+    got = OA.sdpa_decomposition_fp64(q, k, v)
+    assert np.allclose(got, np.repeat(v.numpy(), 2, axis=1))
+
+
+def test_identical_keys_average_values():
+    q, v = _rand((1, 3, 1, 64), 10), _rand((1, 3, 20, 64), 11)
+    k = _rand((1, 3, 1, 64), 12).expand(1, 3, 20, 64)
+    got = OA.sdpa_decomposition_fp64(q, k, v)
+    assert np.allclose(got, v.numpy().mean(axis=2, keepdims=True))
+
+
+def test_dominant_key_limit():
+    """One key with a much larger score takes all the weight."""
+    q = torch.zeros((1, 1, 1, 64), dtype=torch.float64)
+    q[..., 0] = 1.0
+    k = torch.zeros((1, 1, 5, 64), dtype=torch.float64)
+    k[0, 0, 3, 0] = 400.0
+    v = _rand((1, 1, 5, 64), 13)
+    got = OA.sdpa_decomposition_fp64(q, k, v)
+    assert np.allclose(got[0, 0, 0], v[0, 0, 3].numpy())
+
+
+def test_gqa_head_mapping_is_h_div_g():
+    """q head h reads KV head h // g (expand + flatten), not h % Hkv."""
+    q, k, v = _rand((1, 8, 1, 16), 14), _rand((1, 2, 6, 16), 15), _rand((1, 2, 6, 16), 16)
+    got = OA.sdpa_decomposition_fp64(q, k, v)
+    kk = k.repeat_interleave(4, dim=1)
+    vv = v.repeat_interleave(4, dim=1)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, kk, vv)
+    assert np.allclose(got, ref.numpy())
+    kw = k.repeat(1, 4, 1, 1)  # the planted mistake: head h -> h % Hkv
+    vw = v.repeat(1, 4, 1, 1)
+    wrong = torch.nn.functional.scaled_dot_product_attention(q, kw, vw)
+    assert not np.allclose(got, wrong.numpy())
+
+
+def test_empty_context_is_zero_like_torch():
+    q = _rand((1, 4, 1, 8), 17)
+    k = torch.empty((1, 2, 0, 8), dtype=torch.float64)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, k, enable_gqa=True)
+    assert np.array_equal(OA.sdpa_decomposition_fp64(q, k, k), ref.numpy())
+    assert not ref.abs().sum()
+
+
+def test_page_layouts_round_trip_and_closed_form():
+    P, Hkv, D = 3, 2, 128
+    rng = np.random.default_rng(SEED)
+    k_log = rng.integers(0, 1 << 15, (P, Hkv, 64, D)).astype(np.uint16)
+    v_log = rng.integers(0, 1 << 15, (P, Hkv, 64, D)).astype(np.uint16)
+    kd, vd = OA.logical_to_pages(k_log, v_log)
+    # K: sticks along D -> [P, Hkv, D/64, 64 tok, 64]; V: sticks along tokens -> [P, Hkv, D, 64 tok]
+    assert np.array_equal(kd.reshape(P, Hkv, D // 64, 64, 64),
+                          k_log.reshape(P, Hkv, 64, D // 64, 64).transpose(0, 1, 3, 2, 4))
+    assert np.array_equal(vd.reshape(P, Hkv, D, 64), v_log.transpose(0, 1, 3, 2))
+    k2, v2 = OA.pages_to_logical(kd, vd, P, Hkv, D)
+    assert np.array_equal(k2, k_log) and np.array_equal(v2, v_log)
+
+
+def test_paged_reference_equals_dense_sdpa():
+    """Gathering permuted pages by the block table rebuilds the dense sequence."""
+    Hkv, D, ctx = 2, 64, 150
+    rng = np.random.default_rng(3)
+    dense_k = rng.standard_normal((Hkv, 192, D)).astype(np.float32)
+    dense_v = rng.standard_normal((Hkv, 192, D)).astype(np.float32)
+    perm = np.array([2, 0, 1])
+    k_log = np.empty((3, Hkv, 64, D), np.float32)
+    v_log = np.empty((3, Hkv, 64, D), np.float32)
+    for i, p in enumerate(perm):
+        k_log[p] = dense_k[:, 64 * i:64 * i + 64]
+        v_log[p] = dense_v[:, 64 * i:64 * i + 64]
+    q = torch.from_numpy(rng.standard_normal((1, 8, D)).astype(np.float32))
+    got = OA.paged_decode_reference(q, k_log, v_log, [perm], [ctx], 0.125)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q[:, :, None, :], torch.from_numpy(dense_k[None, :, :ctx]), torch.from_numpy(dense_v[None, :, :ctx]),
+        scale=0.125, enable_gqa=True)
+    assert torch.allclose(got, ref[:, :, 0, :], atol=1e-6)
+
+
+def test_page_layout_descriptors_follow_stl_rules():
+    """The oracle's page layouts are valid SpyreTensorLayouts: their DMA
+    plans are single loop nests covering every element once."""
+    P, Hkv, D = 2, 3, 128
+    sizes = [P, Hkv, 64, D]
+    st = OL.contiguous_strides(sizes)
+    for lay in (OA.k_page_layout(P, Hkv, D), OA.v_page_layout(P, Hkv, D)):
+        infos = OL.device_stride_infos(sizes, st, 0, lay.device_size, lay.stride_map, True, st)
+        assert len(infos) == 1 and int(np.prod(infos[0].size)) == P * Hkv * 64 * D
