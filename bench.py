@@ -32,10 +32,11 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak); relayout GB/s"
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per decode_split_kernel launch at split 512, from rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the same counters on
-# a 32 MiB copy kernel (x1.997 and x0.999): 538.3 MB read + 4.2 MB written.
-TRAFFIC_BYTES = 542_500_000
+# HBM bytes per decode_split_list_kernel launch at split 512, from rocprofv3
+# --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the same
+# counters on a 32 MiB copy kernel (x1.9967 and x0.9988): 537.26 MB read +
+# 4.25 MB written (profiles/decode_attention_llama3_8b_b32_ctx4096_hbm_counters.md).
+TRAFFIC_BYTES = 541_510_000
 B, HQ, HKV, D, CTX, PAGE, SPLIT = 32, 32, 8, 128, 4096, 64, 512
 
 
