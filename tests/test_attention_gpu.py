@@ -261,3 +261,22 @@ def test_large_batch_grid_mode(cuda):
     rows = [r for r in rows if lens[r] > 0]
     assert_close(out[rows], oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(64)))
     assert torch.count_nonzero(out[0]) == 0
+
+
+def test_fused_merge_workspace_reuse_across_shapes(cuda):
+    """One workspace reused by calls of different shapes (its split flags and
+    partials left over from earlier calls) gives the same bits as a fresh
+    workspace each time."""
+    import torch_spyre_amd as tsa
+
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=cuda)
+    shapes = [(3, 32, 8, 128, [1000, 70, 2200]), (5, 8, 2, 64, [64, 65, 1, 3000, 512]),
+              (3, 32, 8, 128, [1000, 70, 2200]), (2, 16, 16, 128, [4000, 10])]
+    for i, (B, Hq, Hkv, D, lens) in enumerate(shapes):
+        cache, table, lens_t, q = make_case(cuda, B, Hq, Hkv, D, lens, SEED + 70 + i)
+        t, l = table.to(cuda), lens_t.to(cuda)
+        reused = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=128,
+                                            max_context_len=max(lens), workspace=ws)
+        fresh = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=128,
+                                           max_context_len=max(lens))
+        assert torch.equal(reused.view(torch.int16), fresh.view(torch.int16)), i
