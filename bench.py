@@ -3,15 +3,19 @@ on one MI355X.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
-Workload (a "step"): one decode-attention step -- split-KV pass + merge pass --
-for batch 32, 32 q heads / 8 KV heads, head_dim 128, context 4096 per
-sequence, fp16 K/V ~ N(0,1) in 64-token stick-layout pages, block table a
-seeded permutation of the page pool.  Inputs are resident in HBM before the
-timed region; two KV caches (1.07 GB) alternate so the 256 MB last-level
-cache cannot serve a step from the previous one.
+Workload (a "step"): one decode-attention call for batch 32, 32 q heads /
+8 KV heads, head_dim 128, context 4096 per sequence, fp16 K/V ~ N(0,1) in
+64-token stick-layout pages, block table a seeded permutation of the page
+pool, split 512 tokens per wavefront (a whole sequence per workgroup, so the
+call is one kernel).  Inputs are resident in HBM before the timed region;
+two KV caches (1.07 GB) alternate so the 256 MB last-level cache cannot
+serve a step from the previous one.
 
-Also timed (reported under "relayout"): fp16 [4096, 4096] -> sticks,
-sticks -> row-major, and transpose-restick, rotating 8 buffer pairs.
+Also timed: under "more_configs", the ragged batch (64 sequences, context
+~ U[128, 32768], seeded) and the long-context step (batch 4, 64 q / 8 KV
+heads, append one token at position 131072, attend over 131073 tokens);
+under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
+transpose-restick, rotating 8 buffer pairs.
 
 Timing: HIP events on the stream the kernels are launched on, around K
 back-to-back steps, after W warm-up steps.  GB/s = algorithmic bytes / time.
@@ -34,9 +38,9 @@ METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak); relayout GB/s"
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per decode_split_list_kernel launch at split 512, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the same
-# counters on a 32 MiB copy kernel (x1.9967 and x0.9988): 537.26 MB read +
-# 4.25 MB written (profiles/decode_attention_llama3_8b_b32_ctx4096_hbm_counters.md).
-TRAFFIC_BYTES = 541_510_000
+# counters on a 32 MiB copy kernel (x1.9967 and x0.9988)
+# (profiles/decode_attention_llama3_8b_b32_ctx4096_hbm_counters.md).
+TRAFFIC_BYTES = None
 B, HQ, HKV, D, CTX, PAGE, SPLIT = 32, 32, 8, 128, 4096, 64, 512
 
 
@@ -109,6 +113,66 @@ def cpu_baseline(k_log_pages, v_log_pages, table, q, budget_s=12.0):
     }
 
 
+def more_configs(tsa, dev, stream, steps, warmup, seed):
+    """The ragged batch and the long-context append + attend step, timed the
+    same way (one cache each: both are far larger than the last-level
+    cache)."""
+    import torch
+
+    res = {}
+    g = torch.Generator().manual_seed(seed)
+    gg = torch.Generator(device=dev).manual_seed(seed + 1)
+
+    def paged(lens, Hq, Hkv):
+        pages = [(c + PAGE - 1) // PAGE for c in lens]
+        total = sum(pages)
+        cache = tsa.PagedKVCache(total, Hkv, D, device=dev, zero=False)
+        cache.k.normal_(generator=gg)
+        cache.v.normal_(generator=gg)
+        perm = torch.randperm(total, generator=g).to(torch.int32)
+        table = torch.zeros((len(lens), max(pages)), dtype=torch.int32)
+        k = 0
+        for b, n in enumerate(pages):
+            table[b, :n] = perm[k:k + n]
+            k += n
+        q = torch.randn((len(lens), Hq, D), generator=gg, device=dev).half()
+        return cache, table.to(dev), q, total
+
+    # ragged: 64 sequences, context ~ U[128, 32768]
+    lens = torch.randint(128, 32769, (64,), generator=g).tolist()
+    cache, table, q, total = paged(lens, HQ, HKV)
+    lt = torch.tensor(lens, dtype=torch.int32, device=dev)
+    call = tsa.PagedDecode(q, cache.k, cache.v, table, lt, split_tokens=SPLIT, max_context_len=max(lens))
+    ms = timed(lambda i: call(), steps, warmup, stream)
+    nb = attn_bytes(64, HQ, HKV, D, sum(lens), total)
+    res["ragged_b64_ctx_u128_32768"] = {
+        "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+        "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb,
+        "sum_ctx": sum(lens), "kernels_per_step": call.passes}
+    del cache, call
+
+    # long context: batch 4, 64 q / 8 KV heads, append at 131072, attend 131073
+    B5, HQ5, CTX5 = 4, 64, 131072
+    cache, table, q, total = paged([CTX5 + 1] * B5, HQ5, HKV)
+    lt = torch.full((B5,), CTX5 + 1, dtype=torch.int32, device=dev)
+    pos = torch.full((B5,), CTX5, dtype=torch.int32, device=dev)
+    k_new = torch.randn((B5, HKV, D), generator=gg, device=dev).half()
+    v_new = torch.randn((B5, HKV, D), generator=gg, device=dev).half()
+    call = tsa.PagedDecode(q, cache.k, cache.v, table, lt, split_tokens=SPLIT, max_context_len=CTX5 + 1)
+
+    def step(i):
+        tsa.kv_append(k_new, v_new, cache.k, cache.v, table, pos)
+        call()
+
+    ms = timed(step, steps, warmup, stream)
+    nb = attn_bytes(B5, HQ5, HKV, D, B5 * (CTX5 + 1), total) + 2 * 2 * B5 * HKV * D * 2
+    res["long_ctx_b4_g8_ctx131072_append"] = {
+        "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+        "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb,
+        "kernels_per_step": 1 + call.passes}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,16 +212,20 @@ def main():
     ws = torch.empty(tsa.workspace_bytes(B, HQ, HKV, D, CTX, split), dtype=torch.uint8, device=dev)
     out = torch.empty_like(q)
 
-    # One step = split pass + merge pass, timed back to back.  The dominant
-    # kernel (the split pass) is then timed on its own: K back-to-back
-    # launches between two events on the same stream.
+    # One step = one decode call (one kernel at this shape), timed back to
+    # back.  When a split size makes the call two kernels, the split pass
+    # (the dominant kernel) is also timed on its own for the roofline.
     calls = [tsa.PagedDecode(q, c.k, c.v, t, lens, split_tokens=split, max_context_len=CTX,
                              workspace=ws, out=out) for c, t in zip(caches, tables)]
     ms = timed(lambda i: calls[i & 1](), args.steps, args.warmup, stream)
-    split_ms = timed(lambda i: calls[i & 1].split(), args.steps, args.warmup, stream)
+    if calls[0].passes == 1:
+        split_ms = ms
+    else:
+        split_ms = timed(lambda i: calls[i & 1].split(), args.steps, args.warmup, stream)
     nbytes = attn_bytes(B, HQ, HKV, D, B * CTX, n_pages)
     gbs = nbytes / (ms * 1e-3) / 1e9
     split_gbs = nbytes / (split_ms * 1e-3) / 1e9
+    more = more_configs(tsa, dev, stream, min(args.steps, 50), min(args.warmup, 5), seed)
 
     # ---------------- relayout (config: [4096, 4096] fp16) ----------------
     R = C = 4096
@@ -209,6 +277,7 @@ def main():
                      "frac": round(split_gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,
                      "kernel": "decode_split_list_kernel<128>", "kernel_us": round(split_ms * 1e3, 2),
                      "algorithmic_bytes": nbytes},
+        "more_configs": more,
         "relayout": relayout,
     }
 

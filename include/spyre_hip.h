@@ -141,7 +141,9 @@ int spyre_kv_append_f16(const void* k_new, const void* v_new, void* k_cache, voi
                         const int32_t* positions, int B, int Hkv, int D, int page_size,
                         int64_t num_pages, void* stream);
 
-/* Workspace bytes needed by spyre_paged_decode_attn_f16. */
+/* Workspace bytes needed by spyre_paged_decode_attn_f16: fp32 chunk
+ * partials, B * Hkv * ceil(max_context_len / (8 * split_tokens)) * g * (D + 2)
+ * floats. */
 size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv, int D, int max_context_len,
                                                int split_tokens);
 
@@ -155,6 +157,10 @@ size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv, int D, in
  *   context_lens : int32 [B]; every context_lens[b] <= max_context_len
  *   lse          : optional fp32 [B, Hq] natural-log logsumexp (NULL to skip)
  * D in {64, 128}, page_size 64, g <= 16, split_tokens a multiple of 64.
+ * Each wavefront streams at most split_tokens tokens; a workgroup of 8
+ * covers a chunk of up to 8 * split_tokens.  When max_context_len fits one
+ * chunk this is one kernel and the workspace is not touched; otherwise the
+ * chunks' partials are merged by a second kernel.
  * Empty contexts give zeros (as torch's CPU SDPA does).  Replaces the SDPA
  * overrideable decomposition (torch_spyre/_inductor/decompositions.py:523-609)
  * selected by _fused_sdp_choice (torch_spyre/csrc/attn_utils.cpp:22-37). */
@@ -167,8 +173,9 @@ int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* 
 
 /* The two passes of spyre_paged_decode_attn_f16, for callers that schedule
  * them separately (same arguments and workspace; the merge pass reads what
- * the split pass wrote).  Pass 1 writes per-split partials (unnormalised O,
- * running max, row sum) to the workspace; pass 2 combines them into out/lse.
+ * the split pass wrote).  Pass 1 writes every chunk's partial (unnormalised
+ * O, running max, row sum) to the workspace; pass 2 combines them into
+ * out/lse.
  * No reference counterpart: the reference's SDPA decomposition
  * (torch_spyre/_inductor/decompositions.py:523-609) has no split-KV form. */
 int spyre_paged_decode_attn_split_f16(const void* q, const void* k_cache, const void* v_cache,

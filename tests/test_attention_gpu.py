@@ -126,12 +126,15 @@ def test_gqa_groups(cuda, g):
     assert_close(out, ref)
 
 
-def test_ragged_edges_and_empty(cuda):
-    """Contexts at page and split boundaries, and an empty context (zeros, as
-    torch's CPU SDPA returns)."""
+@pytest.mark.parametrize("split", [512, 64])
+def test_ragged_edges_and_empty(cuda, split):
+    """Contexts at page, split and chunk boundaries, and an empty context
+    (zeros, as torch's CPU SDPA returns).  Split 512: every sequence fits one
+    chunk (one kernel); split 64: chunks of 512 tokens, merge pass for the
+    longer sequences only."""
     lens = [0, 1, 63, 64, 65, 511, 512, 513, 1023, 1024, 1025, 4000]
     cache, table, lens_t, q = make_case(cuda, len(lens), 32, 8, 128, lens, SEED + 99)
-    out, lse = run(cache, table, lens_t, q, cuda, return_lse=True)
+    out, lse = run(cache, table, lens_t, q, cuda, return_lse=True, split_tokens=split)
     rows = [b for b, c in enumerate(lens) if c > 0]
     ref = oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128))
     assert_close(out[rows], ref)
@@ -216,19 +219,22 @@ def test_argument_errors(cuda):
         run(cache, table, lens_t, q, cuda, split_tokens=100)
 
 
-def test_two_pass_api_equals_single_call_bitexact(cuda):
-    """paged_decode_split + paged_decode_merge == paged_decode_attention."""
+@pytest.mark.parametrize("lens", [[700, 64, 1999], [700, 64, 1999, 5000, 0, 2048, 2049]])
+def test_two_pass_api_equals_single_call_bitexact(cuda, lens):
+    """paged_decode_split + paged_decode_merge == paged_decode_attention,
+    both when the single call is one kernel (every context fits one chunk of
+    8 x 256 tokens) and when it merges the longer sequences only."""
     import torch_spyre_amd as tsa
 
-    lens = [700, 64, 1999]
-    cache, table, lens_t, q = make_case(cuda, 3, 32, 8, 128, lens, SEED + 41)
+    B = len(lens)
+    cache, table, lens_t, q = make_case(cuda, B, 32, 8, 128, lens, SEED + 41)
     t, l = table.to(cuda), lens_t.to(cuda)
-    ws = torch.empty(tsa.workspace_bytes(3, 32, 8, 128, max(lens), 256), dtype=torch.uint8, device=cuda)
+    ws = torch.empty(tsa.workspace_bytes(B, 32, 8, 128, max(lens), 256), dtype=torch.uint8, device=cuda)
     one, lse1 = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=256,
                                            max_context_len=max(lens), return_lse=True)
     tsa.paged_decode_split(q, cache.k, cache.v, t, l, ws, split_tokens=256, max_context_len=max(lens))
     two = torch.empty_like(q)
-    lse2 = torch.empty((3, 32), dtype=torch.float32, device=cuda)
+    lse2 = torch.empty((B, 32), dtype=torch.float32, device=cuda)
     tsa.paged_decode_merge(l, ws, two, 8, max(lens), split_tokens=256, lse=lse2)
     assert torch.equal(one.view(torch.int16), two.view(torch.int16))
     assert torch.equal(lse1, lse2)
@@ -250,23 +256,23 @@ def test_prepared_call_matches(cuda):
 
 def test_large_batch_grid_mode(cuda):
     """Batches over 1024 sequences take the grid-mode split kernel; sampled
-    rows (including empty and one-token contexts) against the oracle."""
+    rows (including empty and one-token contexts, and contexts of up to three
+    512-token chunks) against the oracle."""
     g = torch.Generator().manual_seed(SEED + 61)
     B = 1100
-    lens = torch.randint(0, 300, (B,), generator=g).tolist()
-    lens[0], lens[1], lens[2] = 0, 1, 299
+    lens = torch.randint(0, 1200, (B,), generator=g).tolist()
+    lens[0], lens[1], lens[2] = 0, 1, 1199
     cache, table, lens_t, q = make_case(cuda, B, 8, 2, 64, lens, SEED + 62)
-    out = run(cache, table, lens_t, q, cuda, split_tokens=128)
+    out = run(cache, table, lens_t, q, cuda, split_tokens=64)
     rows = [1, 2, 5, 500, 777, B - 1]
     rows = [r for r in rows if lens[r] > 0]
     assert_close(out[rows], oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(64)))
     assert torch.count_nonzero(out[0]) == 0
 
 
-def test_fused_merge_workspace_reuse_across_shapes(cuda):
-    """One workspace reused by calls of different shapes (its split flags and
-    partials left over from earlier calls) gives the same bits as a fresh
-    workspace each time."""
+def test_workspace_reuse_across_shapes(cuda):
+    """One workspace reused by calls of different shapes (partials left over
+    from earlier calls) gives the same bits as a fresh workspace each time."""
     import torch_spyre_amd as tsa
 
     ws = torch.zeros(64 << 20, dtype=torch.uint8, device=cuda)

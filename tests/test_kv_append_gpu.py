@@ -79,3 +79,21 @@ def test_append_then_attend_matches_oracle(cuda):
         kd = cache.k[page].cpu().numpy()
         k_log, _ = OA.pages_to_logical(kd[None], cache.v[page].cpu().numpy()[None], 1, Hkv, D)
         assert np.array_equal(k_log[0][:, p % 64, :], k_new[b].cpu().numpy())
+
+
+def test_config5_long_context_append_full_shape(cuda):
+    """Batch 4, 64 q / 8 KV heads (g = 8), D 128: append the token at position
+    131072 into its stick-layout page, then attend over 131073 tokens (2049
+    pages, several chunks and the merge pass); two rows against the oracle."""
+    import torch_spyre_amd as tsa
+
+    B, Hq, Hkv, D, ctx = 4, 64, 8, 128, 131072
+    cache, table, lens, q = make_case(cuda, B, Hq, Hkv, D, [ctx + 1] * B, SEED + 33, extra_pages=0)
+    gg = torch.Generator(device=cuda).manual_seed(SEED + 34)
+    k_new = torch.randn((B, Hkv, D), generator=gg, device=cuda).half()
+    v_new = torch.randn((B, Hkv, D), generator=gg, device=cuda).half()
+    pos = torch.full((B,), ctx, dtype=torch.int32, device=cuda)
+    tsa.kv_append(k_new, v_new, cache.k, cache.v, table.to(cuda), pos)
+    out = run(cache, table, lens, q, cuda, max_context_len=ctx + 1)
+    rows = [0, 3]
+    assert_close(out[rows], oracle_rows(cache, table, lens, q, rows, 1 / math.sqrt(D)))

@@ -28,6 +28,17 @@ from .layout import DataFormats, SpyreTensorLayout
 from .relayout import _require_cuda, _stream_ptr, to_device_layout
 
 PAGE = 64
+# Wavefronts per decode workgroup: a sequence is cut into chunks of at most
+# CHUNK_WAVES * split_tokens tokens (one workgroup each); a call whose
+# max_context_len fits one chunk runs a single kernel, longer ones add the
+# merge pass.  Equal to kWaves in csrc/decode_attn.hip.
+CHUNK_WAVES = 8
+
+
+def decode_passes(max_context_len: int, split_tokens: int = 512) -> int:
+    """Kernels one decode call launches: 1, or 2 when some context may need
+    more than one chunk (the merge pass then combines the chunks)."""
+    return 1 if max_context_len <= CHUNK_WAVES * split_tokens else 2
 
 
 def k_page_layout(num_pages: int, Hkv: int, D: int) -> SpyreTensorLayout:
@@ -165,8 +176,9 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
 
     q [B, Hq, D] fp16; caches as PagedKVCache; block_table int32 [B, W];
     context_lens int32 [B].  ``max_context_len`` bounds every context (if
-    omitted it is read from context_lens, which synchronises).  Runs the
-    split pass then the merge pass."""
+    omitted it is read from context_lens, which synchronises).  One kernel
+    when max_context_len <= CHUNK_WAVES * split_tokens, else the split pass
+    then the merge pass."""
     a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
                     max_context_len, workspace)
     if out is None:
@@ -186,8 +198,10 @@ class PagedDecode:
 
     Checks shapes, dtypes and the workspace once; each launch then only
     passes the stored device pointers to the library (the tensors must stay
-    alive and keep their storage).  ``split()`` and ``merge()`` launch the
-    two passes separately; ``__call__`` runs both."""
+    alive and keep their storage).  ``__call__`` is the single-call entry
+    (one kernel when max_context_len fits one chunk); ``split()`` and
+    ``merge()`` launch the two passes separately (the split pass then
+    writes every chunk's partial to the workspace)."""
 
     def __init__(self, q, k_cache, v_cache, block_table, context_lens, scale=None,
                  split_tokens: int = 512, max_context_len: Optional[int] = None, workspace=None,
@@ -201,16 +215,22 @@ class PagedDecode:
             raise ValueError("lse must be float32 [B, Hq]")
         self.lse = lse
         self._a = a
+        self.passes = decode_passes(a.max_ctx, a.split)
         L = _lib.lib()
+        self._call_fn = L.spyre_paged_decode_attn_f16
         self._split_fn = L.spyre_paged_decode_attn_split_f16
         self._merge_fn = L.spyre_paged_decode_attn_merge_f16
+        lse_ptr = lse.data_ptr() if lse is not None else None
+        self._call_args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+                           block_table.stride(0), context_lens.data_ptr(), self.out.data_ptr(), lse_ptr,
+                           a.ws.data_ptr(), a.ws_bytes, a.B, a.Hq, a.Hkv, a.D, PAGE, a.num_pages,
+                           a.max_ctx, a.split, a.scale, a.stream)
         self._split_args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
                             block_table.stride(0), context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes,
                             a.B, a.Hq, a.Hkv, a.D, PAGE, a.num_pages, a.max_ctx, a.split, a.scale,
                             a.stream)
         self._merge_args = (context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes, self.out.data_ptr(),
-                            lse.data_ptr() if lse is not None else None, a.B, a.Hq, a.Hkv, a.D,
-                            a.max_ctx, a.split, a.stream)
+                            lse_ptr, a.B, a.Hq, a.Hkv, a.D, a.max_ctx, a.split, a.stream)
 
     def split(self) -> None:
         _lib.check("spyre_paged_decode_attn_split_f16", self._split_fn(*self._split_args))
@@ -220,14 +240,14 @@ class PagedDecode:
         return self.out
 
     def __call__(self) -> torch.Tensor:
-        self.split()
-        return self.merge()
+        _lib.check("spyre_paged_decode_attn_f16", self._call_fn(*self._call_args))
+        return self.out
 
 
 def paged_decode_split(q, k_cache, v_cache, block_table, context_lens, workspace: torch.Tensor,
                        scale: Optional[float] = None, split_tokens: int = 512,
                        max_context_len: Optional[int] = None) -> None:
-    """Pass 1 only: per-split partials into ``workspace``."""
+    """Pass 1 only: every chunk's partial into ``workspace``."""
     a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
                     max_context_len, workspace)
     rc = _lib.lib().spyre_paged_decode_attn_split_f16(

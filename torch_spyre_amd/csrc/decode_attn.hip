@@ -12,11 +12,13 @@
 // operand is built from whole 128-byte sticks loaded straight into VGPRs.
 //
 // Pass 1 (decode_split_list_kernel; decode_split_kernel for batches over
-// kMaxListSeqs): one wavefront per work item (sequence, KV head, split of
-// `split_pages` pages).  The split's pages rotate through the wavefront's
-// operand registers -- the KV carousel: page i+1's K loads are issued as
-// soon as page i's QK MFMAs have consumed their registers, its V loads as
-// soon as PV has -- and each page is
+// kMaxListSeqs): one workgroup of kWaves wavefronts per work item (sequence,
+// KV head, chunk).  A sequence's pages are cut into as few chunks of at most
+// kWaves * split_pages pages as cover it, in equal shares, and each
+// wavefront streams an equal share (at most split_pages) of its chunk.  The
+// pages rotate through the wavefront's operand registers -- the KV carousel:
+// page i+1's K loads are issued as soon as page i's QK MFMAs have consumed
+// their registers, its V loads as soon as PV has -- and each page is
 //   S^T[tok, head] = K[tok, :] Q^T[:, head]   4 x D/32 MFMA 16x16x32 (M = 16 tokens)
 //   online softmax in fp32 (exp2 domain), row max across the 4 lane groups
 //   of a head by lane shuffles;
@@ -24,12 +26,17 @@
 // The q heads of one KV head (g of them, padded to the MFMA's 16 columns)
 // form the dense N dimension, so K and V are read once for all g heads.
 // The token order of the QK rows is permuted so that each lane's P values
-// are exactly the 8 consecutive tokens the PV B operand needs.  The split's
-// partial (unnormalised O, running max, row sum) goes from registers to the
-// workspace; no LDS and no barrier is involved.
+// are exactly the 8 consecutive tokens the PV B operand needs.  The
+// wavefronts' partials (unnormalised O, running max, row sum) are combined
+// in registers through LDS, pairwise in log2(kWaves) rounds.  A sequence
+// that fits one chunk (every sequence when max_context_len <= kWaves *
+// split_tokens) is then finished by its workgroup: fp16 out and LSE are
+// written directly and pass 2 is not launched.  Otherwise the chunk's
+// partial goes to the workspace.
 //
-// Pass 2 (decode_merge_kernel): per (sequence, q head) combine the splits'
-// partials -- the split-KV merge -- and write fp16 out (+ optional LSE).
+// Pass 2 (decode_merge_kernel): per (sequence, q head) with several chunks,
+// combine the chunks' partials -- the split-KV merge -- and write fp16 out
+// (+ optional LSE).
 
 #include <hip/hip_runtime.h>
 
@@ -44,7 +51,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPage = 64;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;  // wavefronts per workgroup = per work item
 constexpr int kThreads = kWaves * 64;
 constexpr int kCols = 16;  // MFMA N: q heads per KV head, padded
 constexpr float kLog2e = 1.4426950408889634f;
@@ -62,10 +69,21 @@ struct SplitArgs {
   int64_t bt_stride;
   const int32_t* ctx_lens;
   float* ws;
+  _Float16* out;  // null: every chunk writes its partial (two-pass mode)
+  float* lse;
   int64_t num_pages;
-  int B, Hq, Hkv, g, max_splits, split_pages, max_ctx;
+  int B, Hq, Hkv, g, max_chunks, chunk_pages, max_ctx;
   float scale_log2;
 };
+
+// Pages of a context and the number of chunks (of at most chunk_pages
+// pages) it is cut into; an empty context still has one chunk, whose
+// workgroup writes its zeros.
+__host__ __device__ __forceinline__ int pages_of(int ctx) { return ctx / kPage + (ctx % kPage != 0); }
+__host__ __device__ __forceinline__ int chunks_of(int ctx, int chunk_pages) {
+  const int p = pages_of(ctx);
+  return p == 0 ? 1 : p / chunk_pages + (p % chunk_pages != 0);
+}
 
 // Work-list mode handles batches up to this many sequences (their split
 // counts are prefix-summed in LDS); larger batches use grid mode.
@@ -176,20 +194,24 @@ __device__ __forceinline__ void load_v(f16x8 (&va)[D / 16][2], Rsrc vr, const Lo
   }
 }
 
-// One work item -- split s of sequence b, KV head kvh -- streamed by one
-// wavefront: its pages rotate through the operand registers (the next page's
-// K loads are issued as soon as this page's QK MFMAs have consumed theirs),
-// and the split's partial (unnormalised O, running max m, row sum l) goes
-// straight from registers to the workspace.  No LDS, no barriers.
+// Pages [p0, p0 + n_it) of sequence b, KV head kvh (context ctx tokens),
+// streamed by one wavefront: the pages rotate through the operand registers
+// (the next page's K loads are issued as soon as this page's QK MFMAs have
+// consumed theirs).  Leaves the wavefront's partial in registers: lane
+// (head col, group grp) holds O^T[d = 16db + 4grp + v][col] unnormalised in
+// o[db][v], the running max m (log2 domain) and the row sum l of head col.
+// n_it = 0 leaves the empty partial (0, -inf, 0).
 template <int D>
-__device__ __forceinline__ void process_item(const SplitArgs& a, int b, int s, int kvh, int lane) {
+__device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh, int p0, int n_it,
+                                             int ctx, int lane, f32x4 (&o)[D / 16], float& m_out,
+                                             float& l_out) {
   constexpr int DS = D / 32;  // QK K-steps
   constexpr int DB = D / 16;  // PV output blocks
-  const int ctx = min(max(a.ctx_lens[b], 0), a.max_ctx);
-  const int n_pages = (ctx + kPage - 1) / kPage;
-  const int p0 = s * a.split_pages;
-  if (p0 >= n_pages) return;
-  const int n_it = min(a.split_pages, n_pages - p0);
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  m_out = -INFINITY;
+  l_out = 0.f;
+  if (n_it <= 0) return;
   const int col = lane & 15, grp = lane >> 4;
   const int32_t* trow = a.block_table + static_cast<int64_t>(b) * a.bt_stride + p0;
   // One lane per page: the page ids of the next 64 pages.
@@ -211,9 +233,6 @@ __device__ __forceinline__ void process_item(const SplitArgs& a, int b, int s, i
   const int64_t head_elems = static_cast<int64_t>(D) * kPage;
   float m_run = -INFINITY, l_run = 0.f;
   bool poisoned = false;  // a block-table entry was out of range
-  f32x4 o[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Page it's K/V resources (page id broadcast from lane it % 64).
   const int head_bytes = static_cast<int>(head_elems * 2);
@@ -312,44 +331,125 @@ __device__ __forceinline__ void process_item(const SplitArgs& a, int b, int s, i
   if (poisoned) l_run = NAN;  // propagates to the merged output: NaN, not a fault
   l_run += wave_xor(l_run, 16);
   l_run += wave_xor(l_run, 32);
+  m_out = m_run;
+  l_out = l_run;
+}
 
-  // Partial of this split: lane (head col, group grp) holds
-  // O^T[d = 16db + 4grp + v][col] -- 16 contiguous bytes per db.
-  if (col < a.g) {
-    const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits + s;
-    float* wo = a.ws + (slot * a.g + col) * D;
+// Combines the kWaves wavefronts' partials of one workgroup, pairwise in
+// log2(kWaves) rounds through LDS: in each round the upper half of the
+// remaining wavefronts stores (o, m, l) lane by lane and the lower half folds
+// it into its registers with the online-softmax rescale.  Lanes of the two
+// wavefronts hold the same (head, d) elements, so the exchange is
+// lane-to-lane.  Wavefront 0 ends with the workgroup's partial.  Every
+// wavefront of the workgroup must call this (it has barriers).
+template <int D>
+__device__ __forceinline__ void combine_waves(f32x4 (&o)[D / 16], float& m, float& l, int wave,
+                                              int lane) {
+  constexpr int DB = D / 16;
+  __shared__ f32x4 s_o[kWaves / 2][DB][64];
+  __shared__ float s_m[kWaves / 2][64], s_l[kWaves / 2][64];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(wo + 16 * db + 4 * grp) = o[db];
-    if (grp == 0) {
-      float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + (slot * a.g + col) * 2;
-      wm[0] = m_run;
-      wm[1] = l_run;
+  for (int half = kWaves / 2; half >= 1; half >>= 1) {
+    if (wave >= half && wave < 2 * half) {
+      const int s = wave - half;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) s_o[s][db][lane] = o[db];
+      s_m[s][lane] = m;
+      s_l[s][lane] = l;
     }
+    __syncthreads();
+    if (wave < half) {
+      const float m2 = s_m[wave][lane], l2 = s_l[wave][lane];
+      const float M = fmaxf(m, m2);
+      // Both empty: M = -inf, and exp2(-inf - -inf) would be NaN.
+      const float a1 = M == -INFINITY ? 0.f : fast_exp2(m - M);
+      const float a2 = M == -INFINITY ? 0.f : fast_exp2(m2 - M);
+      l = l * a1 + l2 * a2;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] = o[db] * a1 + s_o[wave][db][lane] * a2;
+      m = M;
+    }
+    if (half > 1) __syncthreads();  // the slots are stored again next round
   }
 }
 
-// Grid mode: blockIdx = (group of kWaves splits, KV head, sequence); wavefront
-// w takes split kWaves * blockIdx.x + w.  Splits past a sequence's context
-// return at once.
+// Work item (sequence b, chunk c, KV head kvh), run by all kWaves
+// wavefronts of the workgroup.  Wavefront 0 writes the result: fp16 out and
+// LSE when the sequence has one chunk and out is given, else the chunk's
+// partial (O^T rows as 16 contiguous bytes per lane and db; m, l) into the
+// workspace for the merge pass.
+template <int D>
+__device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int kvh, int wave,
+                                         int lane) {
+  constexpr int DB = D / 16;
+  const int ctx_raw = a.ctx_lens[b];
+  const int ctx = min(max(ctx_raw, 0), a.max_ctx);
+  const int n_pages = pages_of(ctx);
+  const int nch = chunks_of(ctx, a.chunk_pages);
+  // Chunk c holds pages [cp0, cp1); wavefront w an equal share of them.
+  const int cp0 = static_cast<int>(static_cast<int64_t>(c) * n_pages / nch);
+  const int cp1 = static_cast<int>(static_cast<int64_t>(c + 1) * n_pages / nch);
+  const int nc = cp1 - cp0;
+  const int w0 = cp0 + static_cast<int>(static_cast<int64_t>(wave) * nc / kWaves);
+  const int w1 = cp0 + static_cast<int>(static_cast<int64_t>(wave + 1) * nc / kWaves);
+  f32x4 o[DB];
+  float m, l;
+  stream_pages<D>(a, b, kvh, w0, w1 - w0, ctx, lane, o, m, l);
+  combine_waves<D>(o, m, l, wave, lane);
+  const int col = lane & 15, grp = lane >> 4;
+  if (wave != 0 || col >= a.g) return;
+  if (a.out && nch == 1) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
+    _Float16* op = a.out + row * D;
+    const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      f16x4 r;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        // Empty context: zeros, as torch's CPU SDPA returns.
+        const float x = ctx == 0 ? 0.f : (bad ? NAN : o[db][v] / l);
+        r[v] = static_cast<_Float16>(x);
+      }
+      *reinterpret_cast<f16x4*>(op + 16 * db + 4 * grp) = r;
+    }
+    if (a.lse && grp == 0) a.lse[row] = ctx == 0 ? -INFINITY : (m + log2f(l)) * kLn2;
+    return;
+  }
+  const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks + c;
+  float* wo = a.ws + (slot * a.g + col) * D;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(wo + 16 * db + 4 * grp) = o[db];
+  if (grp == 0) {
+    float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D + (slot * a.g + col) * 2;
+    wm[0] = m;
+    wm[1] = l;
+  }
+}
+
+// Grid mode: blockIdx = (chunk, KV head, sequence).  Chunks past a
+// sequence's count return at once (the whole workgroup).
 template <int D>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_kernel(SplitArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
-  process_item<D>(a, blockIdx.z, kWaves * blockIdx.x + wave, blockIdx.y, lane);
+  const int b = blockIdx.z, c = blockIdx.x;
+  const int ctx = min(max(a.ctx_lens[b], 0), a.max_ctx);
+  if (c >= chunks_of(ctx, a.chunk_pages)) return;
+  run_item<D>(a, b, c, blockIdx.y, wave, lane);
 }
 
-// Work-list mode: the items (sequence, split, KV head) that exist are
-// numbered densely -- each workgroup prefix-sums the per-sequence split
-// counts in LDS -- and wavefront w of workgroup x takes item 4x + w.  Real
-// items come first, so no workgroup is spent on a split past a sequence's
-// end until all real ones have been dispatched; ragged batches stay
-// balanced.
+// Work-list mode: the items (sequence, chunk, KV head) that exist are
+// numbered densely -- each workgroup prefix-sums the per-sequence chunk
+// counts in LDS -- and workgroup x takes item x.  Real items come first, so
+// no workgroup is spent on a chunk past a sequence's end until all real ones
+// have been dispatched; ragged batches stay balanced.
 template <int D>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_list_kernel(SplitArgs a) {
   __shared__ int s_pre[kMaxListSeqs > 0 ? kMaxListSeqs + 1 : 1];
-  const int split_tokens = a.split_pages * kPage;
   for (int i = threadIdx.x; i < a.B; i += kThreads) {
     const int c = min(max(a.ctx_lens[i], 0), a.max_ctx);
-    s_pre[i + 1] = (c + split_tokens - 1) / split_tokens;
+    s_pre[i + 1] = chunks_of(c, a.chunk_pages);
   }
   if (threadIdx.x == 0) s_pre[0] = 0;
   __syncthreads();
@@ -369,22 +469,19 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_list_ker
     }
   }
   __syncthreads();
-  const int total = s_pre[a.B] * a.Hkv;
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  auto run = [&](int item) {
-    // item is wavefront-uniform; readfirstlane keeps it (and all that
-    // derives from it) in scalar registers.
-    item = __builtin_amdgcn_readfirstlane(item);
-    const int bs = item / a.Hkv, kvh = item - bs * a.Hkv;
-    int lo = 0, hi = a.B;  // s_pre[lo] <= bs < s_pre[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (__builtin_amdgcn_readfirstlane(s_pre[mid]) <= bs) lo = mid; else hi = mid;
-    }
-    process_item<D>(a, lo, bs - __builtin_amdgcn_readfirstlane(s_pre[lo]), kvh, lane);
-  };
-  const int item = blockIdx.x * kWaves + wave;
-  if (item < total) run(item);
+  // Everything below is workgroup-uniform; readfirstlane keeps it in
+  // scalar registers.
+  const int total = __builtin_amdgcn_readfirstlane(s_pre[a.B]) * a.Hkv;
+  const int item = blockIdx.x;
+  if (item >= total) return;  // the whole workgroup
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int bs = item / a.Hkv, kvh = item - bs * a.Hkv;
+  int lo = 0, hi = a.B;  // s_pre[lo] <= bs < s_pre[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (__builtin_amdgcn_readfirstlane(s_pre[mid]) <= bs) lo = mid; else hi = mid;
+  }
+  run_item<D>(a, lo, bs - __builtin_amdgcn_readfirstlane(s_pre[lo]), kvh, wave, lane);
 }
 
 struct MergeArgs {
@@ -392,14 +489,16 @@ struct MergeArgs {
   const int32_t* ctx_lens;
   _Float16* out;
   float* lse;
-  int B, Hq, Hkv, g, max_splits, split_tokens, max_ctx;
+  int B, Hq, Hkv, g, max_chunks, chunk_pages, max_ctx;
+  int skip_single;  // sequences of one chunk were finished by pass 1
 };
 
-// Split-KV merge: one block of D threads per (q head, sequence).  All loads
-// of a chunk of kMergeChunk splits (m, l and the thread's O column) are
-// issued together before any of them is used, so a chunk costs one memory
-// latency; splits past the sequence's count are read (in bounds: the
-// workspace holds max_splits) and discarded by selects, never multiplied.
+// Split-KV merge: one block of D threads per (q head, sequence) over the
+// sequence's chunk partials.  All loads of kMergeChunk chunks (m, l and the
+// thread's O column) are issued together before any of them is used, so
+// they cost one memory latency; chunks past the sequence's count are read
+// (in bounds: the workspace holds max_chunks) and discarded by selects,
+// never multiplied.
 constexpr int kMergeChunk = 16;
 
 template <int D>
@@ -407,26 +506,27 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int kvh = h / a.g, hh = h % a.g;
   const int ctx_raw = a.ctx_lens[b];
-  const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_splits;
-  const float* wo = a.ws + slot0 * a.g * D + hh * D + d;
-  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_splits * a.g * D + slot0 * a.g * 2 + hh * 2;
-  const int64_t so = static_cast<int64_t>(a.g) * D;  // split stride of wo
-  const int sm = 2 * a.g;                              // split stride of wm
   const int ctx = min(max(ctx_raw, 0), a.max_ctx);
-  const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
+  const int ns = chunks_of(ctx, a.chunk_pages);
+  if (a.skip_single && ns == 1) return;
+  const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks;
+  const float* wo = a.ws + slot0 * a.g * D + hh * D + d;
+  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D + slot0 * a.g * 2 + hh * 2;
+  const int64_t so = static_cast<int64_t>(a.g) * D;  // chunk stride of wo
+  const int sm = 2 * a.g;                              // chunk stride of wm
   _Float16* o = a.out + (static_cast<int64_t>(b) * a.Hq + h) * D;
-  if (ns == 0) {  // empty context: zeros, as torch's CPU SDPA returns
+  if (ctx == 0) {  // empty context: zeros, as torch's CPU SDPA returns
     o[d] = static_cast<_Float16>(0.f);
     if (a.lse && d == 0) a.lse[static_cast<int64_t>(b) * a.Hq + h] = -INFINITY;
     return;
   }
-  // Running (M, L, acc) over chunks, rescaled like the online softmax.
+  // Running (M, L, acc) over the chunks, rescaled like the online softmax.
   float M = -INFINITY, L = 0.f, acc = 0.f;
   for (int c = 0; c < ns; c += kMergeChunk) {
     float m[kMergeChunk], l[kMergeChunk], x[kMergeChunk];
 #pragma unroll
     for (int u = 0; u < kMergeChunk; ++u) {
-      const int s = min(c + u, a.max_splits - 1);
+      const int s = min(c + u, a.max_chunks - 1);
       m[u] = wm[s * sm];
       l[u] = wm[s * sm + 1];
       x[u] = wo[s * so];
@@ -435,7 +535,7 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
 #pragma unroll
     for (int u = 0; u < kMergeChunk; ++u)
       if (c + u < ns) mc = fmaxf(mc, m[u]);
-    const float r = fast_exp2(M - mc);  // first chunk: exp2(-inf) = 0
+    const float r = fast_exp2(M - mc);  // first round: exp2(-inf) = 0
     L *= r;
     acc *= r;
 #pragma unroll
@@ -452,8 +552,11 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
   if (a.lse && d == 0) a.lse[static_cast<int64_t>(b) * a.Hq + h] = (M + log2f(L)) * kLn2;
 }
 
-int64_t splits_for(int max_ctx, int split_tokens) {
-  return max_ctx <= 0 ? 1 : (static_cast<int64_t>(max_ctx) + split_tokens - 1) / split_tokens;
+// Chunks of the longest context: a chunk is kWaves wavefronts' shares of at
+// most split_tokens tokens each.
+int64_t max_chunks_for(int max_ctx, int split_tokens) {
+  const int64_t chunk_tokens = static_cast<int64_t>(kWaves) * split_tokens;
+  return max_ctx <= 0 ? 1 : (max_ctx + chunk_tokens - 1) / chunk_tokens;
 }
 
 }  // namespace
@@ -462,8 +565,8 @@ extern "C" size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv
                                                           int max_context_len, int split_tokens) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || split_tokens <= 0 || Hq % Hkv) return 0;
   const int64_t g = Hq / Hkv;
-  const int64_t ns = splits_for(max_context_len, split_tokens);
-  return static_cast<size_t>(B) * Hkv * ns * g * (D + 2) * sizeof(float);
+  const int64_t nc = max_chunks_for(max_context_len, split_tokens);
+  return static_cast<size_t>(B) * Hkv * nc * g * (D + 2) * sizeof(float);
 }
 
 namespace {
@@ -474,6 +577,7 @@ struct Plan {
   dim3 g1, g2;
   int D;
   bool list;
+  bool multi_chunk;  // some context may need more than one chunk
 };
 
 int plan_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
@@ -503,23 +607,28 @@ int plan_attn(const void* q, const void* k_cache, const void* v_cache, const int
       spyre_paged_decode_attn_workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens);
   SPYRE_REQUIRE(workspace_bytes >= need, SPYRE_ENOSPC, "workspace %zu < %zu bytes",
                 workspace_bytes, need);
-  const int max_splits = static_cast<int>(splits_for(max_context_len, split_tokens));
+  SPYRE_REQUIRE(split_tokens <= (1 << 24), SPYRE_EUNSUPPORTED, "split_tokens %d > 2^24",
+                split_tokens);
+  const int64_t max_chunks = max_chunks_for(max_context_len, split_tokens);
+  const int64_t items = static_cast<int64_t>(B) * Hkv * max_chunks;
+  SPYRE_REQUIRE(items < (int64_t{1} << 31) && Hkv <= 65535 && B <= 65535,
+                SPYRE_EUNSUPPORTED, "too many work items (B=%d Hkv=%d chunks=%lld)", B, Hkv,
+                static_cast<long long>(max_chunks));
+  const int chunk_pages = kWaves * (split_tokens / kPage);
   p.sa = SplitArgs{static_cast<const _Float16*>(q), static_cast<const _Float16*>(k_cache),
                    static_cast<const _Float16*>(v_cache), block_table, bt_stride, context_lens,
-                   static_cast<float*>(workspace), num_pages, B, Hq, Hkv, g, max_splits,
-                   split_tokens / kPage, max_context_len, scale * kLog2e};
+                   static_cast<float*>(workspace), static_cast<_Float16*>(out), lse, num_pages, B,
+                   Hq, Hkv, g, static_cast<int>(max_chunks), chunk_pages, max_context_len,
+                   scale * kLog2e};
   p.ma = MergeArgs{static_cast<const float*>(workspace), context_lens, static_cast<_Float16*>(out),
-                   lse, B, Hq, Hkv, g, max_splits, split_tokens, max_context_len};
+                   lse, B, Hq, Hkv, g, static_cast<int>(max_chunks), chunk_pages, max_context_len, 0};
   p.D = D;
   p.list = B <= kMaxListSeqs;
-  if (p.list) {
-    // Upper bound on the items; those past the real count are numbered last
-    // and exit at once.
-    const int64_t wgs = (static_cast<int64_t>(B) * Hkv * max_splits + kWaves - 1) / kWaves;
-    p.g1 = dim3(static_cast<unsigned>(std::max<int64_t>(1, wgs)));
-  } else {
-    p.g1 = dim3((max_splits + kWaves - 1) / kWaves, Hkv, B);
-  }
+  // List mode: an upper bound on the items; those past the real count are
+  // numbered last and exit at once.  Grid mode: (chunk, KV head, sequence).
+  p.g1 = p.list ? dim3(static_cast<unsigned>(items))
+                : dim3(static_cast<unsigned>(max_chunks), Hkv, B);
+  p.multi_chunk = max_chunks > 1;
   p.g2 = dim3(Hq, B);
   return SPYRE_OK;
 }
@@ -574,7 +683,7 @@ extern "C" int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, co
                      const_cast<void*>(workspace), workspace_bytes, B, Hq, Hkv, D, kPage, 1,
                      max_context_len, split_tokens, 1.f, false, true, p);
   if (rc != SPYRE_OK) return rc;
-  return launch_merge(p, static_cast<hipStream_t>(stream));
+  return launch_merge(p, static_cast<hipStream_t>(stream));  // every sequence
 }
 
 extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* v_cache,
@@ -592,5 +701,7 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
   if (rc != SPYRE_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if ((rc = launch_split(p, st)) != SPYRE_OK) return rc;
+  if (!p.multi_chunk) return SPYRE_OK;  // pass 1 wrote every output
+  p.ma.skip_single = 1;
   return launch_merge(p, st);
 }
