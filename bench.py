@@ -240,15 +240,15 @@ def main():
     to_plan = tsa.dma_plan([R, C], [C, 1], [C, 1], 0, dflt, True)
     from_plan = tsa.dma_plan([R, C], [C, 1], [C, 1], 0, dflt, False)
     tr_plan = [tsa.restick_plan([R, C], dflt, trl)]
-    dma = tsa.relayout.dma_copy
     rel_bytes = 2 * R * C * 2
     relayout = {}
-    for name, fn in (
-        ("to_sticks", lambda i: dma(xs[i % nbuf], outs_dev[i % nbuf], to_plan)),
-        ("from_sticks", lambda i: dma(devs[i % nbuf], outs_host[i % nbuf], from_plan)),
-        ("transpose_restick", lambda i: dma(devs[i % nbuf], outs_dev[i % nbuf], tr_plan)),
+    DmaCopy = tsa.relayout.DmaCopy
+    for name, calls in (
+        ("to_sticks", [DmaCopy(xs[i], outs_dev[i], to_plan) for i in range(nbuf)]),
+        ("from_sticks", [DmaCopy(devs[i], outs_host[i], from_plan) for i in range(nbuf)]),
+        ("transpose_restick", [DmaCopy(devs[i], outs_dev[i], tr_plan) for i in range(nbuf)]),
     ):
-        t = timed(fn, args.steps, args.warmup, stream)
+        t = timed(lambda i: calls[i % nbuf](), args.steps, args.warmup, stream)
         relayout[name] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1),
                           "frac": round(rel_bytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     # plain device copy of the same bytes, for reference

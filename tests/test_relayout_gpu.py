@@ -146,6 +146,63 @@ def test_restickify_random_vs_oracle(cuda, sizes, order):
     assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
 
 
+# Shapes whose nests take the 32 x 32-stick tile kernel: partial tiles along
+# both stick loops, and one or two outer loops.
+def test_prepared_dma_copy_matches(cuda):
+    """DmaCopy (validated once, launched repeatedly) == dma_copy."""
+    import torch_spyre_amd as tsa
+
+    sizes = [100, 2112]
+    bits = OR.random_finite_f16_bits(tuple(sizes), SEED + 17)
+    x = _bits_tensor(bits, cuda)
+    stl = tsa.SpyreTensorLayout(sizes, torch.float16)
+    want = tsa.to_device_layout(x, stl)
+    out = torch.zeros_like(want)
+    call = tsa.DmaCopy(x, out, tsa.dma_plan(sizes, [2112, 1], [2112, 1], 0, stl, True))
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+TILE_CASES = [([100, 2112], [0, 1]), ([33, 4096], [0, 1]), ([100, 40, 2112], [0, 1, 2]),
+              ([40, 100, 2112], [1, 0, 2]), ([2, 3, 100, 2112], [2, 1, 0, 3])]
+
+
+@pytest.mark.parametrize("sizes,order", TILE_CASES, ids=lambda v: str(v))
+def test_stick_tile_layouts_vs_oracle(cuda, sizes, order):
+    import torch_spyre_amd as tsa
+
+    strides = OL.contiguous_strides(sizes)
+    stl = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    o = OL.stl_init(sizes, strides, "float16", order)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + sum(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    dev = tsa.to_device_layout(x, stl)
+    want = OL.h2d(bits, sizes, strides, 0, o)
+    assert np.array_equal(_as_bits(dev).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    assert np.array_equal(_as_bits(back).reshape(-1), bits)
+
+
+@pytest.mark.parametrize("sizes", [[104, 2112], [3, 136, 4160], [8, 4096]], ids=str)
+def test_transpose_restick_partial_tiles_vs_oracle(cuda, sizes):
+    """Transpose-restick nests whose 64 x 64 tile counts are not multiples of
+    the four tiles a wavefront takes."""
+    import torch_spyre_amd as tsa
+
+    order = list(range(len(sizes)))
+    order[-2], order[-1] = order[-1], order[-2]
+    strides = OL.contiguous_strides(sizes)
+    src = tsa.SpyreTensorLayout(sizes, torch.float16)
+    dst = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + 11 * len(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    out = tsa.restickify(tsa.to_device_layout(x, src), dst)
+    want = OL.h2d(bits, sizes, strides, 0, OL.stl_init(sizes, strides, "float16", order))
+    assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
+
+
 def test_page_layouts_vs_oracle(cuda):
     """The paged K/V cache layouts built by the relayout engine equal the
     oracle's H2D of the same logical pages."""

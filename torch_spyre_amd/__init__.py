@@ -22,6 +22,7 @@ from .layout import (  # noqa: E402
     restick_plan,
 )
 from .relayout import (  # noqa: E402
+    DmaCopy,
     copy_tensor,
     device_tensor_layout,
     from_device_layout,
@@ -48,7 +49,7 @@ from . import ops  # noqa: E402,F401  (registers the spyre:: ops)
 
 __all__ = [
     "DataFormats", "ElementArrangement", "SpyreTensorLayout", "dma_plan", "get_device_dtype",
-    "restick_plan", "copy_tensor", "device_tensor_layout", "from_device_layout", "overwrite",
+    "restick_plan", "DmaCopy", "copy_tensor", "device_tensor_layout", "from_device_layout", "overwrite",
     "restickify", "spyre_empty_with_layout", "to_device_layout", "transpose_restick_layout",
     "PagedDecode", "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
     "paged_decode_merge", "paged_decode_split",

@@ -59,6 +59,23 @@ def dma_copy(src: torch.Tensor, dst: torch.Tensor, infos, elem_bytes: Optional[i
     _lib.check("spyre_dma_copy", rc)
 
 
+class DmaCopy:
+    """A validated ``dma_copy`` that can be launched repeatedly: the loop-nest
+    array and the pointers are built once, each call only enters the library
+    (the tensors must stay alive and keep their storage)."""
+
+    def __init__(self, src: torch.Tensor, dst: torch.Tensor, infos, elem_bytes: Optional[int] = None):
+        esz = elem_bytes or src.element_size()
+        sp, sb = _storage_span(src)
+        dp, db = _storage_span(dst)
+        self._infos = (_lib.StrideInfo * max(1, len(infos)))(*infos)
+        self._args = (sp, sb, dp, db, esz, self._infos, len(infos), _stream_ptr(dst.device))
+        self._fn = _lib.lib().spyre_dma_copy
+
+    def __call__(self) -> None:
+        _lib.check("spyre_dma_copy", self._fn(*self._args))
+
+
 def _tag(t: torch.Tensor, layout: SpyreTensorLayout, size, stride) -> torch.Tensor:
     t._spyre_layout = layout
     t._spyre_host_size = [int(v) for v in size]
