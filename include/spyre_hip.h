@@ -189,6 +189,37 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
                                       int Hkv, int D, int max_context_len, int split_tokens,
                                       void* stream);
 
+/* Attention mask kinds of spyre_sdpa_fwd_f16. */
+#define SPYRE_MASK_NONE 0
+#define SPYRE_MASK_F16 1  /* additive fp16 bias                */
+#define SPYRE_MASK_F32 2  /* additive fp32 bias                */
+#define SPYRE_MASK_BOOL 3 /* uint8/bool: nonzero = attend      */
+
+/* Workspace bytes needed by spyre_sdpa_fwd_f16: V re-laid out with its
+ * sticks along tokens, B * Hkv * D * ceil(Skv / 64) * 64 fp16. */
+size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
+
+/* Scaled dot-product attention forward (prefill, any Sq):
+ *   out[b,h,i,:] = softmax_j(scale * q[b,h,i,:] . k[b,h/g,j,:] + bias[b,h,i,j]) v[b,h/g,j,:]
+ * q [B,Hq,Sq,D], k/v [B,Hkv,Skv,D] fp16 with feature stride 1 and the other
+ * strides ({b, h, s}, elements) multiples of 8; 16-byte aligned pointers.
+ * bias: none; the mask (kind SPYRE_MASK_*, strides {b, h, i, j} in elements,
+ * 0 to broadcast); or, with is_causal, -inf where j > i (top-left aligned).
+ * A row with every key masked gives zeros and LSE -inf.
+ * out: [B, Sq, Hq, D] contiguous (the layout of the reference's result,
+ * returned as its [B,Hq,Sq,D] transpose); lse: optional fp32 [B, Hq, Sq]
+ * natural-log logsumexp.  D in {64, 128}; g = Hq / Hkv (GQA).
+ * Replaces aten::_scaled_dot_product_fused_attention_overrideable as
+ * decomposed by torch_spyre/_inductor/decompositions.py:523-609 (selected by
+ * _fused_sdp_choice, torch_spyre/csrc/attn_utils.cpp:22-37), whose logsumexp
+ * is left uninitialised (:584-586). */
+int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const void* k,
+                       const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                       const void* attn_mask, int mask_kind, const int64_t* mask_strides,
+                       int is_causal, float scale, void* out, float* lse, void* workspace,
+                       size_t workspace_bytes, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,7 +5,12 @@ Test infrastructure only (see ``oracle/__init__.py``).
 * ``sdpa_decomposition_fp64`` restates the reference's SDPA decomposition
   (torch_spyre/_inductor/decompositions.py:546-609): sqrt(scale) applied to q
   and k (:552-558), GQA by expanding each KV head over its g query heads
-  (:560-563), softmax over keys (:577), then P.V (:591).  Computed in fp64.
+  (:560-563), the causal bias triu(-inf, diagonal=1) over [Sq, Skv] (:567-570),
+  the additive attention bias (:572-573), softmax over keys (:576), then P.V
+  (:591).  Computed in fp64.  A boolean mask is first turned into an additive
+  one (-inf where False), as torch does before it calls the overrideable op.
+  ``return_lse`` adds the natural-log logsumexp of the biased scores (the
+  reference returns an uninitialised tensor there, :584-586).
 * ``sdpa_cpu_fp32`` is the reference's CPU eager path that its tests compare
   against (tests/inductor/utils_inductor.py:662; tests/inductor/test_inductor_ops.py:5386-5392):
   torch.nn.functional.scaled_dot_product_attention on fp32 CPU tensors.
@@ -30,8 +35,19 @@ from . import layout as L
 PAGE = 64
 
 
-def sdpa_decomposition_fp64(q, k, v, scale=None):
-    """q [B, Hq, Sq, D], k/v [B, Hkv, S, D] (numpy or torch) -> fp64 numpy [B, Hq, Sq, D]."""
+def additive_mask(attn_mask):
+    """A boolean mask (True = attend) as the additive bias torch builds from
+    it: 0 where True, -inf where False.  Float masks pass through."""
+    m = np.asarray(attn_mask)
+    if m.dtype == np.bool_:
+        return np.where(m, 0.0, -np.inf)
+    return m.astype(np.float64)
+
+
+def sdpa_decomposition_fp64(q, k, v, scale=None, attn_mask=None, is_causal=False, return_lse=False):
+    """q [B, Hq, Sq, D], k/v [B, Hkv, S, D] (numpy or torch) -> fp64 numpy
+    [B, Hq, Sq, D] (and the logsumexp [B, Hq, Sq] with return_lse).  A row
+    whose keys are all masked gives NaN, as torch.softmax does."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
@@ -46,21 +62,39 @@ def sdpa_decomposition_fp64(q, k, v, scale=None):
         k = np.repeat(k, g, axis=1)  # expand(...).flatten(1, 2): head h reads KV head h // g
         v = np.repeat(v, g, axis=1)
     if k.shape[2] == 0:
-        return np.zeros((B, Hq, Sq, D))
+        out = np.zeros((B, Hq, Sq, D))
+        return (out, np.full((B, Hq, Sq), -np.inf)) if return_lse else out
     att = q @ np.swapaxes(k, -1, -2)
-    att = att - att.max(axis=-1, keepdims=True)
-    p = np.exp(att)
-    p = p / p.sum(axis=-1, keepdims=True)
-    return p @ v
+    if is_causal:
+        assert attn_mask is None
+        att = att + np.triu(np.full(att.shape[-2:], -np.inf), 1)
+    if attn_mask is not None:
+        att = att + additive_mask(attn_mask)
+    mx = att.max(axis=-1, keepdims=True)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(att - mx)
+        tot = e.sum(axis=-1, keepdims=True)
+        out = (e / tot) @ v
+    if not return_lse:
+        return out
+    with np.errstate(divide="ignore", invalid="ignore"):
+        lse = (mx + np.log(tot))[..., 0]
+    return out, lse
 
 
-def sdpa_cpu_fp32(q, k, v, scale=None) -> torch.Tensor:
-    """torch CPU eager SDPA in fp32 (enable_gqa when Hq != Hkv)."""
+def sdpa_cpu_fp32(q, k, v, scale=None, attn_mask=None, is_causal=False) -> torch.Tensor:
+    """torch CPU eager SDPA in fp32 (enable_gqa when Hq != Hkv).  Fully
+    masked rows give zeros here (torch's safe softmax)."""
     q = torch.as_tensor(q).float().cpu()
     k = torch.as_tensor(k).float().cpu()
     v = torch.as_tensor(v).float().cpu()
+    if attn_mask is not None:
+        attn_mask = torch.as_tensor(attn_mask).cpu()
+        if attn_mask.dtype != torch.bool:
+            attn_mask = attn_mask.float()
     gqa = q.shape[1] != k.shape[1]
-    return torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale, enable_gqa=gqa)
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=is_causal,
+                                                            scale=scale, enable_gqa=gqa)
 
 
 def k_page_layout(num_pages, Hkv, D) -> L.Layout:

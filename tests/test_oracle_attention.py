@@ -125,3 +125,71 @@ def test_page_layout_descriptors_follow_stl_rules():
     for lay in (OA.k_page_layout(P, Hkv, D), OA.v_page_layout(P, Hkv, D)):
         infos = OL.device_stride_infos(sizes, st, 0, lay.device_size, lay.stride_map, True, st)
         assert len(infos) == 1 and int(np.prod(infos[0].size)) == P * Hkv * 64 * D
+
+
+# ---- prefill (Sq > 1): causal, masks, logsumexp ----
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D", [(2, 4, 4, 9, 9, 16), (1, 8, 2, 17, 23, 32), (2, 6, 3, 5, 12, 8)])
+def test_prefill_decomposition_matches_torch(B, Hq, Hkv, Sq, Sk, D):
+    q, k, v = _rand((B, Hq, Sq, D), 20), _rand((B, Hkv, Sk, D), 21), _rand((B, Hkv, Sk, D), 22)
+    gqa = Hq != Hkv
+    for causal in (False, True):
+        ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa)
+        got = OA.sdpa_decomposition_fp64(q, k, v, is_causal=causal)
+        assert np.allclose(got, ref.numpy(), atol=1e-12, rtol=1e-10)
+    mask = _rand((Sq, Sk), 23)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=gqa)
+    assert np.allclose(OA.sdpa_decomposition_fp64(q, k, v, attn_mask=mask.numpy()), ref.numpy(), atol=1e-12)
+    assert np.allclose(OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask).numpy(), ref.numpy(), atol=1e-5)
+
+
+def test_causal_equals_explicit_triu_mask_and_bool_mask():
+    """The reference's test pairs is_causal=True with the mask triu(-inf, 1)
+    (tests/inductor/test_inductor_ops.py:2598-2626); a boolean tril mask is
+    the same bias after conversion.  Excluding the diagonal (triu(-inf, 0))
+    is the planted mistake and must differ."""
+    q, k, v = _rand((1, 2, 12, 16), 24), _rand((1, 2, 12, 16), 25), _rand((1, 2, 12, 16), 26)
+    causal = OA.sdpa_decomposition_fp64(q, k, v, is_causal=True)
+    tri = np.triu(np.full((12, 12), -np.inf), 1)
+    assert np.array_equal(causal, OA.sdpa_decomposition_fp64(q, k, v, attn_mask=tri))
+    keep = np.tril(np.ones((12, 12), bool))
+    assert np.array_equal(causal, OA.sdpa_decomposition_fp64(q, k, v, attn_mask=keep))
+    wrong = np.triu(np.full((12, 12), -np.inf), 0)
+    wrong[0, 0] = 0.0  # keep row 0 defined
+    assert not np.allclose(causal, OA.sdpa_decomposition_fp64(q, k, v, attn_mask=wrong))
+
+
+def test_causal_closed_forms():
+    """Row 0 of a causal attention sees key 0 only: out = v[0], lse =
+    scale * q0.k0; the last row of a square causal attention is the
+    unmasked attention of that row."""
+    q, k, v = _rand((1, 1, 6, 8), 27), _rand((1, 1, 6, 8), 28), _rand((1, 1, 6, 8), 29)
+    out, lse = OA.sdpa_decomposition_fp64(q, k, v, scale=0.5, is_causal=True, return_lse=True)
+    assert np.allclose(out[0, 0, 0], v[0, 0, 0].numpy())
+    assert np.isclose(lse[0, 0, 0], 0.5 * float(q[0, 0, 0] @ k[0, 0, 0]))
+    full = OA.sdpa_decomposition_fp64(q, k, v, scale=0.5)
+    assert np.allclose(out[0, 0, -1], full[0, 0, -1])
+
+
+def test_lse_closed_forms():
+    """Identical keys: lse = s + log(n); and lse matches a direct fp64 logsumexp."""
+    q = _rand((1, 1, 3, 8), 30)
+    k = _rand((1, 1, 1, 8), 31).expand(1, 1, 7, 8)
+    v = _rand((1, 1, 7, 8), 32)
+    _, lse = OA.sdpa_decomposition_fp64(q, k, v, scale=0.25, return_lse=True)
+    s = 0.25 * (q[0, 0] @ k[0, 0, 0]).numpy()
+    assert np.allclose(lse[0, 0], s + np.log(7))
+    mask = _rand((3, 7), 33)
+    _, lse2 = OA.sdpa_decomposition_fp64(q, _rand((1, 1, 7, 8), 34), v, attn_mask=mask.numpy(), return_lse=True)
+    kk = _rand((1, 1, 7, 8), 34)[0, 0].numpy()
+    sc = (q[0, 0].numpy() @ kk.T) / math.sqrt(8) + mask.numpy()
+    assert np.allclose(lse2[0, 0], np.log(np.exp(sc).sum(-1)))
+
+
+def test_fully_masked_row_nan_in_decomposition_zero_in_cpu_sdpa():
+    q, k, v = _rand((1, 1, 3, 8), 35), _rand((1, 1, 4, 8), 36), _rand((1, 1, 4, 8), 37)
+    m = np.zeros((3, 4))
+    m[1] = -np.inf
+    assert np.isnan(OA.sdpa_decomposition_fp64(q, k, v, attn_mask=m)[0, 0, 1]).all()
+    cpu = OA.sdpa_cpu_fp32(q, k, v, attn_mask=torch.from_numpy(m))
+    assert not cpu[0, 0, 1].any()

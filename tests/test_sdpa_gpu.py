@@ -1,0 +1,198 @@
+"""GPU parity of the SDPA forward kernel (prefill, causal, masks, GQA,
+logsumexp) against the oracle: torch's CPU eager SDPA in fp32 (the
+reference's compare path) and the fp64 restatement of the reference's
+decomposition.
+
+Bar: fp16 outputs within |gpu - ref| <= 2e-3 + 1e-2 |ref| elementwise; LSE
+within 2e-3 absolute of the fp64 logsumexp.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from tests.conftest import SEED
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-2
+LSE_ATOL = 2e-3
+
+
+def assert_close(got, ref):
+    got = got.float().cpu()
+    ref = torch.as_tensor(ref).float().cpu()
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert not torch.isnan(got).any(), "NaN in output"
+    err = (got - ref).abs()
+    bad = err > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())} elements out of tolerance; max abs err {err.max():.3e}"
+
+
+def randn(shape, seed, dtype=torch.float16):
+    return torch.randn(shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float32).to(dtype)
+
+
+def ref_case(B, Sq, Skv, Hq, Hkv, D, seed):
+    """q/k/v as the reference's test builds them: [B, S, H, D] tensors viewed
+    as [B, H, S, D] (tests/inductor/test_inductor_ops.py:2576-2650)."""
+    q = randn((B, Sq, Hq, D), seed).transpose(1, 2)
+    k = randn((B, Skv, Hkv, D), seed + 1).transpose(1, 2)
+    v = randn((B, Skv, Hkv, D), seed + 2).transpose(1, 2)
+    return q, k, v
+
+
+def run(cuda, q, k, v, **kw):
+    import torch_spyre_amd as tsa
+
+    mask = kw.pop("attn_mask", None)
+    if mask is not None:
+        mask = mask.to(cuda)
+    return tsa.scaled_dot_product_attention(q.to(cuda), k.to(cuda), v.to(cuda), attn_mask=mask, **kw)
+
+
+# The reference's prefill parameter sets (tests/inductor/test_inductor_ops.py:2576-2650):
+# q/k/v (2, 256, H, 128) fp16 transposed to (2, H, 256, 128).
+REF_SETS = {
+    "mha_prefill": (32, dict()),
+    "mha_prefill_causal": (32, dict(is_causal=True)),
+    "mha_prefill_mask": (32, dict(attn_mask=torch.triu(torch.ones((256, 256), dtype=torch.float16) * -float("inf"),
+                                                      diagonal=1))),
+    "gqa_prefill": (8, dict(enable_gqa=True)),
+    "gqa_prefill_causal": (8, dict(is_causal=True, enable_gqa=True)),
+}
+
+
+@pytest.mark.parametrize("name", list(REF_SETS))
+def test_reference_prefill_sets(cuda, name):
+    Hkv, kw = REF_SETS[name]
+    q, k, v = ref_case(2, 256, 256, 32, Hkv, 128, SEED + len(name))
+    out, lse = run(cuda, q, k, v, return_lse=True, **kw)
+    mask = kw.get("attn_mask")
+    causal = kw.get("is_causal", False)
+    ref = OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask, is_causal=causal)
+    assert_close(out, ref)
+    ref64, lse64 = OA.sdpa_decomposition_fp64(q, k, v, attn_mask=None if mask is None else mask.numpy(),
+                                              is_causal=causal, return_lse=True)
+    assert_close(out, ref64)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+    # the result has the strides of a contiguous [B, S, H, D] tensor (the reference's API promise)
+    assert out.shape == (2, 32, 256, 128) and out.stride() == (256 * 32 * 128, 128, 32 * 128, 1)
+
+
+@pytest.mark.parametrize("Sq,Skv", [(1, 1), (1, 300), (37, 100), (100, 37), (64, 64), (65, 129), (200, 513)])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_ragged_lengths(cuda, Sq, Skv, D, causal):
+    q = randn((2, 4, Sq, D), SEED + Sq)
+    k = randn((2, 2, Skv, D), SEED + Skv)
+    v = randn((2, 2, Skv, D), SEED + Skv + 1)
+    out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, is_causal=causal))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, is_causal=causal, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("g", [1, 2, 4, 8, 16])
+def test_gqa_groups(cuda, g):
+    q = randn((1, 2 * g, 70, 128), SEED + g)
+    k = randn((1, 2, 90, 128), SEED + g + 1)
+    v = randn((1, 2, 90, 128), SEED + g + 2)
+    assert_close(run(cuda, q, k, v, enable_gqa=True), OA.sdpa_cpu_fp32(q, k, v))
+
+
+@pytest.mark.parametrize("kind", ["f16", "f32", "bool"])
+@pytest.mark.parametrize("shape", ["qk", "b1qk", "1h1k"])
+def test_masks_broadcast(cuda, kind, shape):
+    """Additive fp16 / fp32 and boolean masks, broadcast from [Sq, Skv],
+    [B, 1, Sq, Skv] and [1, Hq, 1, Skv] (a padding mask)."""
+    B, Hq, Sq, Skv = 2, 4, 50, 77
+    q, k, v = randn((B, Hq, Sq, 64), SEED + 1), randn((B, Hq, Skv, 64), SEED + 2), randn((B, Hq, Skv, 64), SEED + 3)
+    dims = {"qk": (Sq, Skv), "b1qk": (B, 1, Sq, Skv), "1h1k": (1, Hq, 1, Skv)}[shape]
+    g = torch.Generator().manual_seed(SEED + 4)
+    if kind == "bool":
+        mask = torch.rand(dims, generator=g) > 0.3
+        mask[..., 0] = True  # no fully masked row here
+    else:
+        mask = (torch.randn(dims, generator=g) * 2).to(torch.float16 if kind == "f16" else torch.float32)
+    out = run(cuda, q, k, v, attn_mask=mask)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask))
+
+
+def test_fully_masked_rows_give_zeros_and_minus_inf_lse(cuda):
+    q, k, v = randn((1, 2, 40, 64), SEED + 5), randn((1, 2, 33, 64), SEED + 6), randn((1, 2, 33, 64), SEED + 7)
+    mask = torch.zeros((40, 33))
+    mask[3] = -float("inf")
+    mask[39] = -float("inf")
+    out, lse = run(cuda, q, k, v, attn_mask=mask, return_lse=True)
+    ref = OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask)
+    assert_close(out, ref)
+    assert not out[:, :, 3].float().abs().sum() and not out[:, :, 39].float().abs().sum()
+    assert torch.isinf(lse[:, :, 3]).all() and (lse[:, :, 3] < 0).all()
+
+
+def test_empty_keys_give_zeros(cuda):
+    q = randn((1, 2, 5, 64), SEED + 8)
+    k = torch.empty((1, 2, 0, 64), dtype=torch.float16)
+    out = run(cuda, q, k, k)
+    assert out.shape == (1, 2, 5, 64) and not out.float().abs().sum()
+
+
+def test_scale_applied_once(cuda):
+    q, k, v = randn((1, 4, 30, 128), SEED + 9), randn((1, 4, 45, 128), SEED + 10), randn((1, 4, 45, 128), SEED + 11)
+    assert_close(run(cuda, q, k, v, scale=0.3), OA.sdpa_cpu_fp32(q, k, v, scale=0.3))
+
+
+def test_unaligned_views_are_accepted(cuda):
+    """A head-dim slice of a wider tensor (rows not 16-byte multiples apart)
+    is copied into kernel form first; the result is unchanged."""
+    base = randn((1, 2, 50, 136), SEED + 12)
+    q = base[..., 4:132]
+    k, v = randn((1, 2, 60, 128), SEED + 13), randn((1, 2, 60, 128), SEED + 14)
+    assert_close(run(cuda, q, k, v), OA.sdpa_cpu_fp32(q, k, v))
+
+
+def test_overrideable_tuple_and_custom_op(cuda):
+    import torch_spyre_amd as tsa
+
+    q, k, v = ref_case(1, 100, 100, 8, 2, 64, SEED + 15)
+    q, k, v = q.to(cuda), k.to(cuda), v.to(cuda)
+    res = tsa.sdpa_overrideable(q, k, v, None, 0.0, True)
+    assert len(res) == 9 and res[2] is None and res[3] is None and res[8] is None
+    assert res[4] == 100 and res[5] == 100 and res[1].shape == (1, 8, 100) and res[1].dtype == torch.float32
+    ref = OA.sdpa_cpu_fp32(q, k, v, is_causal=True)
+    assert_close(res[0], ref)
+    out, lse = torch.ops.spyre.sdpa_fwd(q, k, v, None, True, None, True)
+    assert torch.equal(out, res[0]) and torch.equal(lse, res[1])
+
+
+def test_argument_errors(cuda):
+    import torch_spyre_amd as tsa
+
+    q, k, v = randn((1, 4, 8, 64), 1).to(cuda), randn((1, 2, 8, 64), 2).to(cuda), randn((1, 2, 8, 64), 3).to(cuda)
+    with pytest.raises(ValueError):
+        tsa.scaled_dot_product_attention(q, k, v)  # GQA without enable_gqa
+    with pytest.raises(tsa.Unsupported):
+        tsa.scaled_dot_product_attention(q, k, v, dropout_p=0.1, enable_gqa=True)
+    with pytest.raises(ValueError):
+        tsa.scaled_dot_product_attention(q, k, v, attn_mask=torch.zeros(8, 8, device=cuda), is_causal=True,
+                                         enable_gqa=True)
+    q96, k96 = randn((1, 2, 8, 96), 4).to(cuda), randn((1, 2, 8, 96), 5).to(cuda)
+    with pytest.raises(tsa._lib.SpyreHipError):
+        tsa.scaled_dot_product_attention(q96, k96, k96)  # head_dim 96
+
+
+def test_llama3_8b_prefill_1024_causal_sampled_heads(cuda):
+    """Batch 1, 32 q / 8 KV heads, D 128, 1024 tokens, causal: four heads
+    (two KV groups) against the oracle."""
+    q = randn((1, 32, 1024, 128), SEED + 20)
+    k = randn((1, 8, 1024, 128), SEED + 21)
+    v = randn((1, 8, 1024, 128), SEED + 22)
+    out = run(cuda, q, k, v, is_causal=True, enable_gqa=True).cpu()
+    for h in (0, 3, 17, 31):
+        ref = OA.sdpa_cpu_fp32(q[:, h:h + 1], k[:, h // 4:h // 4 + 1], v[:, h // 4:h // 4 + 1], is_causal=True)
+        assert_close(out[:, h:h + 1], ref)

@@ -45,6 +45,11 @@ from .attention import (  # noqa: E402
     v_page_layout,
     workspace_bytes,
 )
+from .sdpa import (  # noqa: E402
+    Unsupported,
+    scaled_dot_product_attention,
+    sdpa_overrideable,
+)
 from . import ops  # noqa: E402,F401  (registers the spyre:: ops)
 
 __all__ = [
@@ -54,4 +59,5 @@ __all__ = [
     "PagedDecode", "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
     "paged_decode_merge", "paged_decode_split",
     "sdpa_decode", "v_page_layout", "workspace_bytes",
+    "Unsupported", "scaled_dot_product_attention", "sdpa_overrideable",
 ]

@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libspyre_hip.so")
-SOURCES = ["layout.cpp", "dma.hip", "decode_attn.hip", "kv_append.hip"]
+SOURCES = ["layout.cpp", "dma.hip", "decode_attn.hip", "kv_append.hip", "sdpa_fwd.hip"]
 ARCH = os.environ.get("SPYRE_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

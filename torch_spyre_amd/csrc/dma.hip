@@ -39,6 +39,7 @@
 #include <vector>
 
 #include "spyre_common.h"
+#include "transpose8.h"
 
 namespace {
 
@@ -242,18 +243,7 @@ __device__ __forceinline__ void transpose_block(u32x4 (&r)[16 / ESZ], u32x4 (&o)
 
 template <>
 __device__ __forceinline__ void transpose_block<2>(u32x4 (&r)[8], u32x4 (&o)[8]) {
-  // r[b] holds elements a = 0..7 of row b; o[a] gets elements b = 0..7 of column a.
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(r);
-  uint32_t* x = reinterpret_cast<uint32_t*>(o);
-#pragma unroll
-  for (int a = 0; a < 8; ++a) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t lo = w[(2 * p) * 4 + a / 2];
-      const uint32_t hi = w[(2 * p + 1) * 4 + a / 2];
-      x[a * 4 + p] = (a & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-    }
-  }
+  spyre_hip::transpose8x8_b16(r, o);
 }
 
 template <>

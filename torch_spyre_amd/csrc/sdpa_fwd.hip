@@ -1,0 +1,407 @@
+// Scaled dot-product attention forward for gfx950 (spyre_sdpa_fwd_f16):
+// prefill and any Sq, with GQA, causal masking or an additive / boolean mask,
+// and the natural-log logsumexp.
+//
+// Semantics (torch_spyre/_inductor/decompositions.py:523-609, with torch's
+// CPU SDPA as the numerical reference):
+//   out[b,h,i,:] = softmax_j(scale * q[b,h,i,:] . k[b,h/g,j,:] + bias[b,h,i,j]) v[b,h/g,j,:]
+// bias = 0, or the mask (boolean masks keep where true), or for causal
+// attention -inf where j > i (top-left aligned, triu(diagonal=1)).  A row
+// whose keys are all masked gives zeros and LSE -inf (torch's CPU result;
+// the reference's torch.softmax would give NaN there).
+//
+// Two kernels on the caller's stream:
+//  1. v_token_sticks_kernel: V [B, Hkv, Skv, D] (rows may be strided) ->
+//     Vt [B, Hkv, D, S64] in the workspace: V with its sticks along tokens
+//     (the transpose-restick of each head), zero-padded to S64 = ceil(Skv /
+//     64) * 64.  This makes the PV product's reduction dim (keys) contiguous,
+//     as the paged decode cache stores V.
+//  2. sdpa_fwd_kernel: one wavefront per 32 queries of one (sequence, q
+//     head), four per workgroup, streaming 64 keys per step:
+//       S^T[key, q] = K[key, :] Q^T[:, q]   4 x D/32 x 2 MFMA 16x16x32
+//       online softmax in fp32 (exp2 domain) per query column;
+//       O^T[d, q] += Vt[d, key] P^T[key, q]   D/16 x 2 x 2 MFMA 16x16x32
+//     The keys of the S rows are permuted so that each lane's P values are
+//     the 8 consecutive keys the PV operand needs (no lane exchange).
+//     Causal attention stops each wavefront at its last query's key.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+#include "spyre_common.h"
+#include "transpose8.h"
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+using spyre_hip::u32x4_t;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kQ = 32;      // queries per wavefront (two MFMA column tiles)
+constexpr int kKeys = 64;   // keys per step
+constexpr int kStick = 64;  // Vt token padding
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float wave_xor(float x, int m) { return __shfl_xor(x, m, 64); }
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// K and Vt are read with buffer loads: the (sequence, head) base and extent
+// in SGPRs, a 32-bit per-lane byte offset in one VGPR, the load-invariant
+// part in an SGPR / immediate.  Accesses past the extent read zeros.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit format
+
+__device__ __forceinline__ Rsrc make_rsrc(const _Float16* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), 0, bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ f16x8 bload(Rsrc r, int voff, int soff) {
+  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// S^T block jh (16 keys of the step): MFMA row i <-> key 32(jh/2) + 8(i/4) + 4(jh%2) + i%4.
+__device__ __forceinline__ int key_of(int jh, int i) {
+  return 32 * (jh >> 1) + 8 * (i >> 2) + 4 * (jh & 1) + (i & 3);
+}
+
+// ---- 1. V -> token sticks -------------------------------------------------
+
+struct VtArgs {
+  const _Float16* v;
+  int64_t sb, sh, ss;  // V strides (elements); d stride 1
+  _Float16* vt;        // [B, Hkv, D, s64]
+  int Hkv, Skv, s64, D;
+  int64_t tiles;       // 64 x 64 tiles
+};
+
+// One wavefront per 64 tokens x 64 features: each lane loads an 8 x 8 block
+// as eight 16-byte token rows, transposes it in registers and stores eight
+// 16-byte feature rows of Vt.  Tokens past Skv are written as zeros.
+__global__ __launch_bounds__(kThreads) void v_token_sticks_kernel(VtArgs a) {
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / 64;
+  if (tile >= a.tiles) return;
+  const int lane = threadIdx.x % 64;
+  const int ts_n = a.s64 / 64, td_n = a.D / 64;
+  const int ts = static_cast<int>(tile % ts_n);
+  const int64_t r = tile / ts_n;
+  const int td = static_cast<int>(r % td_n);
+  const int64_t bh = r / td_n;
+  const int64_t b = bh / a.Hkv, kvh = bh % a.Hkv;
+  const int s0 = ts * 64 + (lane / 8) * 8, d0 = td * 64 + (lane % 8) * 8;
+  const _Float16* src = a.v + b * a.sb + kvh * a.sh + d0;
+  u32x4_t x[8], y[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int s = s0 + t;
+    x[t] = s < a.Skv ? *reinterpret_cast<const u32x4_t*>(src + s * a.ss) : u32x4_t{0, 0, 0, 0};
+  }
+  spyre_hip::transpose8x8_b16(x, y);
+  _Float16* dst = a.vt + (bh * a.D + d0) * a.s64 + s0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4_t*>(dst + e * a.s64) = y[e];
+}
+
+// ---- 2. attention -----------------------------------------------------------
+
+enum MaskKind { kNoMask = 0, kMaskF16 = 1, kMaskF32 = 2, kMaskBool = 3 };
+
+struct FwdArgs {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* vt;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t vt_sb, vt_sh;
+  uint32_t k_bytes, vt_bytes;  // extent of one (sequence, KV head) of K / Vt
+  const void* mask;
+  int64_t m_sb, m_sh, m_sq, m_sk;
+  _Float16* out;  // [B, Sq, Hq, D]
+  float* lse;     // [B, Hq, Sq] or null
+  int B, Hq, Hkv, g, Sq, Skv, s64, mask_kind, causal;
+  float scale_log2;
+};
+
+// Mask element types by kind.
+template <int MK> struct MaskElem { using T = uint8_t; };
+template <> struct MaskElem<kMaskF16> { using T = _Float16; };
+template <> struct MaskElem<kMaskF32> { using T = float; };
+
+// Additive bias (log2 domain) of mask element x.
+template <int MK>
+__device__ __forceinline__ float bias_of(typename MaskElem<MK>::T x) {
+  if constexpr (MK == kMaskBool)
+    return x ? 0.f : -INFINITY;
+  else
+    return static_cast<float>(x) * kLog2e;
+}
+
+// MK: mask kind (a separate kernel each, so the unmasked one carries no mask code).
+template <int D, int MK>
+__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(FwdArgs a) {
+  constexpr int DS = D / 32;  // QK k-steps
+  constexpr int DT = D / 16;  // O row tiles
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int q0 = (blockIdx.x * kWaves + wave) * kQ;
+  if (q0 >= a.Sq) return;
+  const int kvh = h / a.g;
+  const int col = lane & 15, grp = lane >> 4;
+  const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh;
+  const Rsrc kr = make_rsrc(a.k + b * a.k_sb + kvh * a.k_sh, a.k_bytes);
+  const Rsrc vr = make_rsrc(a.vt + b * a.vt_sb + kvh * a.vt_sh, a.vt_bytes);
+
+  // Q^T operands: lane (query column col, feature group grp).
+  f16x8 qb[2][DS];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int qi = q0 + 16 * nt + col;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+      qb[nt][ds] = qi < a.Sq ? *reinterpret_cast<const f16x8*>(qp + qi * a.q_ss + 32 * ds + 8 * grp)
+                             : f16x8{};
+  }
+
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  f32x4 o[2][DT];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Mask rows of this lane's two query columns (clamped into the mask).
+  using MT = typename MaskElem<MK>::T;
+  const MT* mrow[2] = {nullptr, nullptr};
+  if constexpr (MK != kNoMask) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int qc = min(q0 + 16 * nt + col, a.Sq - 1);
+      mrow[nt] = static_cast<const MT*>(a.mask) + b * a.m_sb + h * a.m_sh + qc * a.m_sq;
+    }
+  }
+  const int m_sk = static_cast<int>(a.m_sk);
+
+  // Per-lane byte offsets: K row key_of(jh, col) (+ 16-byte feature group),
+  // Vt row col (+ 8 keys of group grp).  Keys past Skv are masked below;
+  // their K rows are clamped to the last row.
+  const int vt_lane = (col * a.s64 + 8 * grp) * 2;
+  // Causal: no key past this wavefront's last query is needed.
+  const int key_end = a.causal ? min(a.Skv, q0 + kQ) : a.Skv;
+  for (int kb = 0; kb < key_end; kb += kKeys) {
+    f16x8 ka[4][DS];
+#pragma unroll
+    for (int jh = 0; jh < 4; ++jh) {
+      const int key = min(kb + key_of(jh, col), a.Skv - 1);
+      const int voff = static_cast<int>(key * a.k_ss * 2) + 16 * grp;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) ka[jh][ds] = bload(kr, voff, 64 * ds);
+    }
+    f32x4 sc[4][2];
+#pragma unroll
+    for (int jh = 0; jh < 4; ++jh) {
+      sc[jh][0] = sc[jh][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        sc[jh][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[0][ds], sc[jh][0], 0, 0, 0);
+        sc[jh][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[1][ds], sc[jh][1], 0, 0, 0);
+      }
+    }
+    // The K registers are free: the Vt operands load during the softmax.
+    f16x8 va[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) va[dt][j] = bload(vr, vt_lane + kb * 2, (16 * dt * a.s64 + 32 * j) * 2);
+    // Lane (query column, group grp) holds keys kb + 32j + 8grp + 4h + v.
+    f16x8 pb[2][2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int qi = q0 + 16 * nt + col;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jh = 0; jh < 4; ++jh)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int key = kb + 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
+          bool keep = key < a.Skv && qi < a.Sq;
+          if (a.causal) keep = keep && key <= qi;
+          float x = sc[jh][nt][v] * a.scale_log2;
+          if constexpr (MK != kNoMask) x += bias_of<MK>(mrow[nt][min(key, a.Skv - 1) * m_sk]);
+          x = keep ? x : -INFINITY;
+          sc[jh][nt][v] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, wave_xor(mx, 16));
+      mx = fmaxf(mx, wave_xor(mx, 32));
+      const float m_new = fmaxf(m_run[nt], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // all masked so far: p = 0
+      const float alpha = fast_exp2(m_run[nt] - m_use);
+      float psum = 0.f;
+#pragma unroll
+      for (int jh = 0; jh < 4; ++jh)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float p = fast_exp2(sc[jh][nt][v] - m_use);
+          psum += p;
+          pb[nt][jh >> 1][(jh & 1) * 4 + v] = static_cast<_Float16>(p);
+        }
+      l_run[nt] = l_run[nt] * alpha + psum;
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= alpha;
+    }
+    // O^T += Vt[d, keys] P^T[keys, q]; Vt is zero past Skv (up to s64).
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt][j], pb[0][j], o[0][dt], 0, 0, 0);
+        o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt][j], pb[1][j], o[1][dt], 0, 0, 0);
+      }
+  }
+
+  // Lane (query column, group grp) holds O^T[d = 16dt + 4grp + v][q].
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    float l = l_run[nt];
+    l += wave_xor(l, 16);
+    l += wave_xor(l, 32);
+    const int qi = q0 + 16 * nt + col;
+    if (qi >= a.Sq) continue;
+    _Float16* op = a.out + ((static_cast<int64_t>(b) * a.Sq + qi) * a.Hq + h) * D;
+    const float inv = l > 0.f ? 1.f / l : 0.f;  // every key masked: zeros
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      f16x4 r;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) r[v] = static_cast<_Float16>(o[nt][dt][v] * inv);
+      *reinterpret_cast<f16x4*>(op + 16 * dt + 4 * grp) = r;
+    }
+    if (a.lse && grp == 0)
+      a.lse[(static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi] =
+          l > 0.f ? (m_run[nt] + log2f(l)) * kLn2 : -INFINITY;
+  }
+}
+
+int64_t s64_of(int Skv) { return (static_cast<int64_t>(Skv) + kStick - 1) / kStick * kStick; }
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+extern "C" size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D) {
+  if (B <= 0 || Hkv <= 0 || Skv < 0 || D <= 0) return 0;
+  return static_cast<size_t>(B) * Hkv * D * s64_of(Skv) * sizeof(_Float16);
+}
+
+extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const void* k,
+                                  const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                  const void* attn_mask, int mask_kind, const int64_t* mask_strides,
+                                  int is_causal, float scale, void* out, float* lse,
+                                  void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
+                                  int Sq, int Skv, int D, void* stream) {
+  spyre_hip::clear_error();
+  SPYRE_REQUIRE(q_strides && k_strides && v_strides, SPYRE_EINVAL, "null stride argument");
+  SPYRE_REQUIRE((Sq == 0 || (q && out)) && (Skv == 0 || (k && v)), SPYRE_EINVAL,
+                "null pointer argument");
+  SPYRE_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Sq >= 0 && Skv >= 0, SPYRE_EINVAL,
+                "bad shape B=%d Hq=%d Hkv=%d Sq=%d Skv=%d", B, Hq, Hkv, Sq, Skv);
+  SPYRE_REQUIRE(D == 64 || D == 128, SPYRE_EUNSUPPORTED, "head_dim %d not in {64, 128}", D);
+  SPYRE_REQUIRE(mask_kind >= kNoMask && mask_kind <= kMaskBool, SPYRE_EINVAL, "bad mask kind %d",
+                mask_kind);
+  SPYRE_REQUIRE(mask_kind == kNoMask || (attn_mask && mask_strides), SPYRE_EINVAL,
+                "mask pointer / strides missing");
+  SPYRE_REQUIRE(!(is_causal && mask_kind != kNoMask), SPYRE_EINVAL,
+                "is_causal and an attention mask are exclusive");
+  SPYRE_REQUIRE(B <= 65535 && Hq <= 65535, SPYRE_EUNSUPPORTED, "B or Hq above 65535");
+  // 16-byte rows: every operand row is read as whole 16-byte vectors.
+  SPYRE_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), SPYRE_EINVAL,
+                "q, k, v, out must be 16-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    SPYRE_REQUIRE(q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 &&
+                      q_strides[i] >= 0 && k_strides[i] >= 0 && v_strides[i] >= 0,
+                  SPYRE_EINVAL, "q/k/v strides must be non-negative multiples of 8 elements");
+  if (mask_kind != kNoMask) {
+    for (int i = 0; i < 4; ++i)
+      SPYRE_REQUIRE(mask_strides[i] >= 0, SPYRE_EINVAL, "negative mask stride");
+    SPYRE_REQUIRE(static_cast<int64_t>(Skv) * mask_strides[3] < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
+                  "mask row spans 2^31 elements or more");
+  }
+  const size_t need = spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D);
+  SPYRE_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
+                SPYRE_ENOSPC, "workspace %zu < %zu bytes (or misaligned)", workspace_bytes, need);
+  if (Sq == 0) return SPYRE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int s64 = static_cast<int>(s64_of(Skv));
+  if (Skv > 0) {
+    VtArgs va{static_cast<const _Float16*>(v), v_strides[0], v_strides[1], v_strides[2],
+              static_cast<_Float16*>(workspace), Hkv, Skv, s64, D,
+              static_cast<int64_t>(B) * Hkv * (s64 / 64) * (D / 64)};
+    const int64_t blocks = (va.tiles + kWaves - 1) / kWaves;
+    SPYRE_REQUIRE(blocks < (int64_t{1} << 31), SPYRE_EUNSUPPORTED, "V too large");
+    v_token_sticks_kernel<<<dim3(static_cast<unsigned>(blocks)), kThreads, 0, st>>>(va);
+    const hipError_t e = hipGetLastError();
+    SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "V restick launch failed: %s", hipGetErrorString(e));
+  }
+  FwdArgs fa{};
+  fa.q = static_cast<const _Float16*>(q);
+  fa.k = static_cast<const _Float16*>(k);
+  fa.vt = static_cast<const _Float16*>(workspace);
+  fa.q_sb = q_strides[0];
+  fa.q_sh = q_strides[1];
+  fa.q_ss = q_strides[2];
+  fa.k_sb = k_strides[0];
+  fa.k_sh = k_strides[1];
+  fa.k_ss = k_strides[2];
+  fa.vt_sb = static_cast<int64_t>(Hkv) * D * s64;
+  fa.vt_sh = static_cast<int64_t>(D) * s64;
+  // Buffer extents (bytes) of one head: K rows 0..Skv-1, Vt [D, s64].
+  const int64_t k_span = Skv > 0 ? ((static_cast<int64_t>(Skv) - 1) * k_strides[2] + D) * 2 : 0;
+  const int64_t vt_span = static_cast<int64_t>(D) * s64 * 2;
+  SPYRE_REQUIRE(k_span < (int64_t{1} << 31) && vt_span < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
+                "one head of K or V spans 2 GiB or more");
+  fa.k_bytes = static_cast<uint32_t>(k_span);
+  fa.vt_bytes = static_cast<uint32_t>(vt_span);
+  fa.mask = attn_mask;
+  fa.mask_kind = mask_kind;
+  if (mask_kind != kNoMask) {
+    fa.m_sb = mask_strides[0];
+    fa.m_sh = mask_strides[1];
+    fa.m_sq = mask_strides[2];
+    fa.m_sk = mask_strides[3];
+  }
+  fa.out = static_cast<_Float16*>(out);
+  fa.lse = lse;
+  fa.B = B;
+  fa.Hq = Hq;
+  fa.Hkv = Hkv;
+  fa.g = Hq / Hkv;
+  fa.Sq = Sq;
+  fa.Skv = Skv;
+  fa.s64 = s64;
+  fa.causal = is_causal ? 1 : 0;
+  fa.scale_log2 = scale * kLog2e;
+  const dim3 grid((Sq + kWaves * kQ - 1) / (kWaves * kQ), Hq, B);
+  auto launch = [&](auto mk) {
+    constexpr int MK = decltype(mk)::value;
+    if (D == 128)
+      sdpa_fwd_kernel<128, MK><<<grid, kThreads, 0, st>>>(fa);
+    else
+      sdpa_fwd_kernel<64, MK><<<grid, kThreads, 0, st>>>(fa);
+  };
+  switch (mask_kind) {
+    case kMaskF16: launch(std::integral_constant<int, kMaskF16>{}); break;
+    case kMaskF32: launch(std::integral_constant<int, kMaskF32>{}); break;
+    case kMaskBool: launch(std::integral_constant<int, kMaskBool>{}); break;
+    default: launch(std::integral_constant<int, kNoMask>{}); break;
+  }
+  const hipError_t e = hipGetLastError();
+  SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "sdpa launch failed: %s", hipGetErrorString(e));
+  return SPYRE_OK;
+}

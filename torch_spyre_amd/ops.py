@@ -12,16 +12,19 @@ an op on CPU tensors raises.  Fake kernels make the ops traceable.
   spyre::kv_append            batched paged-cache write (no reference counterpart)
   spyre::paged_decode_attention    paged split-KV decode (no reference counterpart;
                               semantics of torch_spyre/_inductor/decompositions.py:523-609)
+  spyre::sdpa_fwd             SDPA forward with logsumexp (the overrideable op's
+                              decomposition, torch_spyre/_inductor/decompositions.py:523-609)
 """
 
 from __future__ import annotations
 
 import math
-from typing import Sequence
+from typing import Optional, Sequence
 
 import torch
 
 from . import attention, relayout
+from . import sdpa as _sdpa
 from .layout import DataFormats, SpyreTensorLayout, get_device_dtype
 
 _CUDA = ("cuda",)
@@ -118,3 +121,18 @@ def _(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens=512, m
 
 __all__ = ["to_device_layout", "from_device_layout", "restickify", "overwrite", "overwrite_f",
            "kv_append", "paged_decode_attention", "DataFormats"]
+
+
+@torch.library.custom_op("spyre::sdpa_fwd", mutates_args=(), device_types=_CUDA)
+def sdpa_fwd(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, attn_mask: Optional[torch.Tensor],
+             is_causal: bool, scale: Optional[float], enable_gqa: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    out, lse = _sdpa.scaled_dot_product_attention(query, key, value, attn_mask=attn_mask, is_causal=is_causal,
+                                                   scale=scale, enable_gqa=enable_gqa, return_lse=True)
+    return out.clone(), lse
+
+
+@sdpa_fwd.register_fake
+def _(query, key, value, attn_mask, is_causal, scale, enable_gqa):
+    B, Hq, Sq, D = query.shape
+    out = query.new_empty((B, Sq, Hq, D)).transpose(1, 2)
+    return out, query.new_empty((B, Hq, Sq), dtype=torch.float32)

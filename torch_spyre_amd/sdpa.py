@@ -1,0 +1,124 @@
+"""Scaled dot-product attention forward (prefill and any query length).
+
+Mirrors ``torch.nn.functional.scaled_dot_product_attention`` and the
+reference's overrideable op ``aten::_scaled_dot_product_fused_attention_overrideable``
+(torch_spyre/_inductor/decompositions.py:523-609, chosen by
+``_fused_sdp_choice`` in torch_spyre/csrc/attn_utils.cpp:22-37):
+
+* GQA by head: q head h reads KV head h // (Hq // Hkv) (:560-563);
+* ``is_causal``: the bias triu(-inf, diagonal=1) over [Sq, Skv], top-left
+  aligned (:565-570); it excludes an explicit mask (the reference asserts);
+* ``attn_mask`` / ``attn_bias``: an additive fp16/fp32 bias or a boolean
+  keep-mask, broadcast to [B, Hq, Sq, Skv];
+* dropout raises ``Unsupported``, as the reference does (:578-580);
+* the output has the strides of a contiguous [B, Sq, Hq, D] tensor viewed as
+  [B, Hq, Sq, D] (the reference's "API promise", :593-596);
+* the logsumexp is real (natural log, [B, Hq, Sq] fp32); the reference
+  leaves it uninitialised (:584-586).
+
+A row whose keys are all masked gives zeros (torch's CPU SDPA), not the NaN
+of the reference's plain softmax.  All work runs in the HIP kernels of
+``spyre_sdpa_fwd_f16``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .relayout import _require_cuda, _stream_ptr
+
+MASK_NONE, MASK_F16, MASK_F32, MASK_BOOL = 0, 1, 2, 3
+_MASK_KIND = {torch.float16: MASK_F16, torch.float32: MASK_F32, torch.bool: MASK_BOOL, torch.uint8: MASK_BOOL}
+
+
+class Unsupported(RuntimeError):
+    """An SDPA feature the device path does not implement (the reference's
+    ``torch_spyre._inductor.errors.Unsupported``, errors.py:16)."""
+
+
+def workspace_bytes(B: int, Hkv: int, Skv: int, D: int) -> int:
+    return int(_lib.lib().spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D))
+
+
+def _operand(t: torch.Tensor, name: str) -> torch.Tensor:
+    """fp16 CUDA [B, H, S, D] whose rows the kernel can read as 16-byte
+    vectors (feature stride 1, other strides multiples of 8, 16-byte
+    aligned); anything else is copied into that form first."""
+    _require_cuda(t, name)
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be 4-D [B, H, S, D]")
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name} must be float16 (got {t.dtype})")
+    ok = t.stride(3) == 1 and all(t.stride(i) % 8 == 0 for i in range(3)) and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
+
+
+def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                 attn_mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                                 is_causal: bool = False, scale: Optional[float] = None,
+                                 enable_gqa: bool = False, return_lse: bool = False,
+                                 workspace: Optional[torch.Tensor] = None):
+    """``F.scaled_dot_product_attention`` on fp16 CUDA tensors: query
+    [B, Hq, Sq, D], key/value [B, Hkv, Skv, D], D in {64, 128}."""
+    q = _operand(query, "query")
+    k = _operand(key, "key")
+    v = _operand(value, "value")
+    B, Hq, Sq, D = q.shape
+    Bk, Hkv, Skv, Dk = k.shape
+    if tuple(v.shape) != (Bk, Hkv, Skv, Dk) or Bk != B or Dk != D:
+        raise ValueError("key/value must be [B, Hkv, Skv, D] matching query")
+    if Hq != Hkv and not enable_gqa:
+        raise ValueError("Hq != Hkv requires enable_gqa=True")
+    if Hq % Hkv:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if dropout_p > 0.0:
+        raise Unsupported("Attention dropout not implemented")
+    if is_causal and attn_mask is not None:
+        raise ValueError("is_causal and attn_mask are exclusive")
+    kind, mask, mstrides = MASK_NONE, None, None
+    if attn_mask is not None:
+        m = torch.as_tensor(attn_mask, device=q.device)
+        if m.dtype not in _MASK_KIND:
+            raise TypeError(f"attn_mask dtype {m.dtype} not supported (float16, float32, bool)")
+        kind = _MASK_KIND[m.dtype]
+        mask = m.expand(B, Hq, Sq, Skv)
+        if mask.dtype == torch.bool:
+            mask = mask.view(torch.uint8)
+        mstrides = _lib.i64_array(mask.stride())
+    s = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    out = torch.empty((B, Sq, Hq, D), dtype=torch.float16, device=q.device)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
+    need = workspace_bytes(B, Hkv, Skv, D)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, need {need}")
+    rc = _lib.lib().spyre_sdpa_fwd_f16(
+        q.data_ptr(), _lib.i64_array(q.stride()[:3]), k.data_ptr(), _lib.i64_array(k.stride()[:3]),
+        v.data_ptr(), _lib.i64_array(v.stride()[:3]), mask.data_ptr() if mask is not None else None,
+        kind, mstrides, int(bool(is_causal)), s, out.data_ptr(),
+        lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), B, Hq, Hkv, Sq, Skv, D, _stream_ptr(q.device))
+    _lib.check("spyre_sdpa_fwd_f16", rc)
+    out = out.transpose(1, 2)
+    return (out, lse) if return_lse else out
+
+
+def sdpa_overrideable(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                      attn_bias: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                      is_causal: bool = False, return_debug_mask: bool = False,
+                      scale: Optional[float] = None):
+    """The 9-tuple of ``_scaled_dot_product_fused_attention_overrideable``
+    (torch_spyre/_inductor/decompositions.py:523-609): (output, logsumexp,
+    cum_seq_q, cum_seq_k, max_q, max_k, philox_seed, philox_offset,
+    debug_attn_mask).  GQA follows from the head counts."""
+    out, lse = scaled_dot_product_attention(query, key, value, attn_mask=attn_bias, dropout_p=dropout_p,
+                                            is_causal=is_causal, scale=scale,
+                                            enable_gqa=query.shape[1] != key.shape[1], return_lse=True)
+    seed = torch.empty((1,), dtype=torch.float16, device=query.device)
+    offset = torch.empty((1,), dtype=torch.float16, device=query.device)
+    return out, lse, None, None, query.shape[2], key.shape[2], seed, offset, None
