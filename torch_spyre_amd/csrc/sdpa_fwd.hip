@@ -289,6 +289,241 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(FwdArgs a) {
   }
 }
 
+// ---- 3. attention with K/V tiles shared through LDS (no mask) -------------
+//
+// One workgroup of kWaves2 wavefronts per 256 queries of one (sequence, q
+// head); wavefront w takes 32 of them.  Each 64-key step, the workgroup
+// stages the K tile [64 keys][D] and the Vt tile [D][64 keys] once in LDS
+// (double-buffered: the next tile's global loads are in flight during this
+// tile's math), and every wavefront reads its MFMA operands from there:
+//   S^T[key, q] = K Q^T   2 x D/16 MFMA 32x32x16 (M = 32 keys, N = 32 queries)
+//   O^T[d, q] += Vt P^T   D/32 x 4 MFMA 32x32x16
+// LDS rows are padded by 16 bytes so that the 16 rows one operand read
+// touches fall in distinct bank groups.  Workgroups are numbered so that
+// those of one (sequence, KV head) run on one XCD (one L2), and for causal
+// attention each head's latest (heaviest) query block starts first.
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves2 = 8;
+constexpr int kThreads2 = kWaves2 * 64;
+constexpr int kQW = 32;             // queries per wavefront
+constexpr int kQB = kWaves2 * kQW;  // queries per workgroup
+constexpr int kKT = 64;             // keys per tile
+constexpr int kPadH = 8;            // LDS row padding, halves (16 bytes)
+
+template <int D>
+struct Lds2 {
+  static constexpr int kRowK = D + kPadH;    // K tile row (one key), halves
+  static constexpr int kRowV = kKT + kPadH;  // Vt tile row (one feature), halves
+  static constexpr int kK = kKT * kRowK;
+  static constexpr int kStage = kK + D * kRowV;
+  static constexpr int kChunksK = kKT * D / 8;  // 16-byte chunks per tile
+  static constexpr int kChunks = 2 * kChunksK;  // K and Vt
+  static constexpr int kPer = kChunks / kThreads2;
+  static_assert(kChunksK % kThreads2 == 0, "K chunks must split evenly over the threads");
+};
+
+// Key of row rho of a 32-key S^T tile.  Lane half h (lanes 32h..32h+31)
+// holds rows 8i + 4h + v (i, v < 4); they are the keys 16(i/2) + 8h +
+// 4(i%2) + v, i.e. the two 8-key runs the PV operand of half h needs.
+__device__ __forceinline__ int key32_of(int rho) {
+  const int i = rho >> 3, h = (rho >> 2) & 1, v = rho & 3;
+  return 16 * (i >> 1) + 8 * h + 4 * (i & 1) + v;
+}
+
+struct Fwd2Args {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* vt;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t vt_sb, vt_sh;
+  _Float16* out;
+  float* lse;
+  int B, Hq, Hkv, g, Sq, Skv, s64, causal, qblocks;
+  uint32_t n_items;
+  int xcd_remap;
+  float scale_log2;
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
+  using L = Lds2<D>;
+  constexpr int DK = D / 16;  // QK k-steps
+  constexpr int DM = D / 32;  // O row tiles
+  __shared__ __align__(16) _Float16 lds[2 * L::kStage];
+
+  // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * g + gi: the
+  // blocks of one (sequence, KV head) are consecutive, latest query block
+  // (longest, under causal masking) first across its g q heads.
+  uint32_t item = blockIdx.x;
+  if (a.xcd_remap) item = (item % 8) * (a.n_items / 8) + item / 8;
+  const int gi = static_cast<int>(item % a.g);
+  uint32_t r = item / a.g;
+  const int qb = a.qblocks - 1 - static_cast<int>(r % a.qblocks);
+  r /= a.qblocks;
+  const int kvh = static_cast<int>(r % a.Hkv);
+  const int b = static_cast<int>(r / a.Hkv);
+  const int h = kvh * a.g + gi;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int qw0 = qb * kQB, q0 = qw0 + wave * kQW;
+  const int col = lane & 31, half = lane >> 5;
+  const int qi = q0 + col;
+  const bool q_ok = qi < a.Sq;
+
+  // Q^T operand: lane (query column, half) holds features 16ks + 8half .. +8.
+  f16x8 qv[DK];
+  {
+    const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(qi, a.Sq - 1)) * a.q_ss + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < DK; ++ks) qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
+  }
+  const _Float16* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
+  const _Float16* vbase = a.vt + b * a.vt_sb + kvh * a.vt_sh;
+
+  // Tile loads: chunk c = thread + kThreads2 * j; chunks [0, kChunksK) are K
+  // rows (keys past Skv read as zeros), the rest Vt rows (zero-padded in the
+  // workspace up to s64, and kb + 64 <= s64).
+  u32x4_t stage_regs[L::kPer];
+  auto load_tile = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < L::kPer; ++j) {
+      const int c = threadIdx.x + j * kThreads2;
+      if (j * kThreads2 < L::kChunksK) {
+        const int row = c / (D / 8), c8 = c % (D / 8), key = kb + row;
+        stage_regs[j] = key < a.Skv ? *reinterpret_cast<const u32x4_t*>(kbase + key * a.k_ss + c8 * 8)
+                                    : u32x4_t{0, 0, 0, 0};
+      } else {
+        const int cv = c - L::kChunksK, drow = cv / (kKT / 8), c8 = cv % (kKT / 8);
+        stage_regs[j] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<int64_t>(drow) * a.s64 + kb + c8 * 8);
+      }
+    }
+  };
+  auto store_tile = [&](int stage) {
+    _Float16* base = lds + stage * L::kStage;
+#pragma unroll
+    for (int j = 0; j < L::kPer; ++j) {
+      const int c = threadIdx.x + j * kThreads2;
+      if (j * kThreads2 < L::kChunksK) {
+        const int row = c / (D / 8), c8 = c % (D / 8);
+        *reinterpret_cast<u32x4_t*>(base + row * L::kRowK + c8 * 8) = stage_regs[j];
+      } else {
+        const int cv = c - L::kChunksK, drow = cv / (kKT / 8), c8 = cv % (kKT / 8);
+        *reinterpret_cast<u32x4_t*>(base + L::kK + drow * L::kRowV + c8 * 8) = stage_regs[j];
+      }
+    }
+  };
+
+  const int key_end = a.causal ? min(a.Skv, qw0 + kQB) : a.Skv;
+  const int n_tiles = (key_end + kKT - 1) / kKT;
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 o[DM];
+#pragma unroll
+  for (int dm = 0; dm < DM; ++dm) o[dm] = f32x16{};
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    const int kb = t * kKT;
+    const bool more = t + 1 < n_tiles;
+    if (more) load_tile(kb + kKT);  // in flight during this tile's math
+    const _Float16* kt = lds + (t & 1) * L::kStage;
+    const _Float16* vt = kt + L::kK;
+    // Causal: a tile past this wavefront's last query is all masked.
+    const bool active = q0 < a.Sq && (!a.causal || kb <= q0 + kQW - 1);
+    if (active) {
+      f32x16 sc[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        sc[mt] = f32x16{};
+        const _Float16* krow = kt + (mt * 32 + key32_of(col)) * L::kRowK + 8 * half;
+#pragma unroll
+        for (int ks = 0; ks < DK; ++ks) {
+          const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + 16 * ks);
+          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[ks], sc[mt], 0, 0, 0);
+        }
+      }
+      // Lane (query column, half) holds rows 8i + 4half + v (register 4i + v).
+      // Only tiles crossing Skv or the causal diagonal need the key test.
+      const bool edge = kb + kKT > a.Skv || (a.causal && kb + kKT - 1 > q0);
+      float mx = -INFINITY;
+      if (edge) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            const int key = kb + mt * 32 + key32_of(8 * (rr >> 2) + 4 * half + (rr & 3));
+            bool keep = key < a.Skv;
+            if (a.causal) keep = keep && key <= qi;
+            const float x = keep ? sc[mt][rr] * a.scale_log2 : -INFINITY;
+            sc[mt][rr] = x;
+            mx = fmaxf(mx, x);
+          }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            const float x = sc[mt][rr] * a.scale_log2;
+            sc[mt][rr] = x;
+            mx = fmaxf(mx, x);
+          }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - m_use);
+      f16x8 pb[4];
+      float psum = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+          const float p = fast_exp2(sc[mt][rr] - m_use);
+          psum += p;
+          const int i = rr >> 2;
+          pb[mt * 2 + (i >> 1)][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
+        }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+#pragma unroll
+      for (int dm = 0; dm < DM; ++dm) {
+        const _Float16* vrow = vt + (dm * 32 + col) * L::kRowV + 8 * half;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + 16 * ks);
+          o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[ks], o[dm], 0, 0, 0);
+        }
+      }
+    }
+    if (more) store_tile((t + 1) & 1);
+    __syncthreads();
+  }
+
+  float l = l_run + __shfl_xor(l_run, 32, 64);
+  if (!q_ok) return;
+  _Float16* op = a.out + ((static_cast<int64_t>(b) * a.Sq + qi) * a.Hq + h) * D;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  // Lane (query column, half) holds O^T rows d = 32dm + 8i + 4half + v.
+#pragma unroll
+  for (int dm = 0; dm < DM; ++dm)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f16x4 rv;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) rv[v] = static_cast<_Float16>(o[dm][4 * i + v] * inv);
+      *reinterpret_cast<f16x4*>(op + 32 * dm + 8 * i + 4 * half) = rv;
+    }
+  if (a.lse && half == 0)
+    a.lse[(static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi] = l > 0.f ? (m_run + log2f(l)) * kLn2 : -INFINITY;
+}
+
 int64_t s64_of(int Skv) { return (static_cast<int64_t>(Skv) + kStick - 1) / kStick * kStick; }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -387,19 +622,54 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
   fa.s64 = s64;
   fa.causal = is_causal ? 1 : 0;
   fa.scale_log2 = scale * kLog2e;
-  const dim3 grid((Sq + kWaves * kQ - 1) / (kWaves * kQ), Hq, B);
-  auto launch = [&](auto mk) {
-    constexpr int MK = decltype(mk)::value;
+  if (mask_kind == kNoMask) {
+    // K/V tiles shared through LDS.
+    Fwd2Args f2{};
+    f2.q = fa.q;
+    f2.k = fa.k;
+    f2.vt = fa.vt;
+    f2.q_sb = fa.q_sb;
+    f2.q_sh = fa.q_sh;
+    f2.q_ss = fa.q_ss;
+    f2.k_sb = fa.k_sb;
+    f2.k_sh = fa.k_sh;
+    f2.k_ss = fa.k_ss;
+    f2.vt_sb = fa.vt_sb;
+    f2.vt_sh = fa.vt_sh;
+    f2.out = fa.out;
+    f2.lse = fa.lse;
+    f2.B = B;
+    f2.Hq = Hq;
+    f2.Hkv = Hkv;
+    f2.g = fa.g;
+    f2.Sq = Sq;
+    f2.Skv = Skv;
+    f2.s64 = s64;
+    f2.causal = fa.causal;
+    f2.qblocks = (Sq + kQB - 1) / kQB;
+    const int64_t items = static_cast<int64_t>(B) * Hq * f2.qblocks;
+    SPYRE_REQUIRE(items < (int64_t{1} << 31), SPYRE_EUNSUPPORTED, "too many query blocks");
+    f2.n_items = static_cast<uint32_t>(items);
+    f2.xcd_remap = items % 8 == 0;
+    f2.scale_log2 = fa.scale_log2;
     if (D == 128)
-      sdpa_fwd_kernel<128, MK><<<grid, kThreads, 0, st>>>(fa);
+      sdpa_fwd_lds_kernel<128><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
     else
-      sdpa_fwd_kernel<64, MK><<<grid, kThreads, 0, st>>>(fa);
-  };
-  switch (mask_kind) {
-    case kMaskF16: launch(std::integral_constant<int, kMaskF16>{}); break;
-    case kMaskF32: launch(std::integral_constant<int, kMaskF32>{}); break;
-    case kMaskBool: launch(std::integral_constant<int, kMaskBool>{}); break;
-    default: launch(std::integral_constant<int, kNoMask>{}); break;
+      sdpa_fwd_lds_kernel<64><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+  } else {
+    const dim3 grid((Sq + kWaves * kQ - 1) / (kWaves * kQ), Hq, B);
+    auto launch = [&](auto mk) {
+      constexpr int MK = decltype(mk)::value;
+      if (D == 128)
+        sdpa_fwd_kernel<128, MK><<<grid, kThreads, 0, st>>>(fa);
+      else
+        sdpa_fwd_kernel<64, MK><<<grid, kThreads, 0, st>>>(fa);
+    };
+    switch (mask_kind) {
+      case kMaskF16: launch(std::integral_constant<int, kMaskF16>{}); break;
+      case kMaskF32: launch(std::integral_constant<int, kMaskF32>{}); break;
+      default: launch(std::integral_constant<int, kMaskBool>{}); break;
+    }
   }
   const hipError_t e = hipGetLastError();
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "sdpa launch failed: %s", hipGetErrorString(e));
