@@ -378,6 +378,10 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(qi, a.Sq - 1)) * a.q_ss + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < DK; ++ks) qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
+    // Wait for Q here, outside the loop: otherwise the first MFMA of every
+    // step also waits for the next tile's loads, which are then in flight.
+#pragma unroll
+    for (int ks = 0; ks < DK; ++ks) asm volatile("" : : "v"(qv[ks]));
   }
   const _Float16* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
   const _Float16* vbase = a.vt + b * a.vt_sb + kvh * a.vt_sh;
@@ -436,17 +440,17 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     // Causal: a tile past this wavefront's last query is all masked.
     const bool active = q0 < a.Sq && (!a.causal || kb <= q0 + kQW - 1);
     if (active) {
-      f32x16 sc[2];
+      // The two key halves' accumulators alternate, so consecutive MFMAs
+      // are independent.
+      f32x16 sc[2] = {f32x16{}, f32x16{}};
+      const _Float16* krow = kt + key32_of(col) * L::kRowK + 8 * half;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        sc[mt] = f32x16{};
-        const _Float16* krow = kt + (mt * 32 + key32_of(col)) * L::kRowK + 8 * half;
+      for (int ks = 0; ks < DK; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < DK; ++ks) {
-          const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + 16 * ks);
+        for (int mt = 0; mt < 2; ++mt) {
+          const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + mt * 32 * L::kRowK + 16 * ks);
           sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[ks], sc[mt], 0, 0, 0);
         }
-      }
       // Lane (query column, half) holds rows 8i + 4half + v (register 4i + v).
       // Only tiles crossing Skv or the causal diagonal need the key test.
       const bool edge = kb + kKT > a.Skv || (a.causal && kb + kKT - 1 > q0);
@@ -492,15 +496,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       m_run = m_new;
 #pragma unroll
       for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+      const _Float16* vrow = vt + col * L::kRowV + 8 * half;
 #pragma unroll
-      for (int dm = 0; dm < DM; ++dm) {
-        const _Float16* vrow = vt + (dm * 32 + col) * L::kRowV + 8 * half;
+      for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + 16 * ks);
+        for (int dm = 0; dm < DM; ++dm) {
+          const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + dm * 32 * L::kRowV + 16 * ks);
           o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[ks], o[dm], 0, 0, 0);
         }
-      }
     }
     if (more) store_tile((t + 1) & 1);
     __syncthreads();
