@@ -147,6 +147,16 @@ def test_scale_applied_once(cuda):
     assert_close(run(cuda, q, k, v, scale=0.3), OA.sdpa_cpu_fp32(q, k, v, scale=0.3))
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.2])
+@pytest.mark.parametrize("causal", [False, True])
+def test_zero_and_negative_scale(cuda, scale, causal):
+    """scale 0 averages the visible values; a negative scale flips the
+    scores (the kernel folds the sign into q)."""
+    q, k, v = randn((1, 4, 70, 64), SEED + 40), randn((1, 4, 90, 64), SEED + 41), randn((1, 4, 90, 64), SEED + 42)
+    assert_close(run(cuda, q, k, v, scale=scale, is_causal=causal),
+                 OA.sdpa_cpu_fp32(q, k, v, scale=scale, is_causal=causal))
+
+
 def test_unaligned_views_are_accepted(cuda):
     """A head-dim slice of a wider tensor (rows not 16-byte multiples apart)
     is copied into kernel form first; the result is unchanged."""

@@ -377,7 +377,10 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   {
     const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(qi, a.Sq - 1)) * a.q_ss + 8 * half;
 #pragma unroll
-    for (int ks = 0; ks < DK; ++ks) qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
+    for (int ks = 0; ks < DK; ++ks) {
+      qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
+      if (a.scale_log2 < 0.f) qv[ks] = -qv[ks];  // the scale's sign, exactly
+    }
     // Wait for Q here, outside the loop: otherwise the first MFMA of every
     // step also waits for the next tile's loads, which are then in flight.
 #pragma unroll
@@ -421,6 +424,9 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 
   const int key_end = a.causal ? min(a.Skv, qw0 + kQB) : a.Skv;
   const int n_tiles = (key_end + kKT - 1) / kKT;
+  // |scale| (its sign is folded into Q), kept above 0 so that masked scores
+  // (-inf) stay -inf; a scale of 0 then gives the uniform weights it should.
+  const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[DM];
 #pragma unroll
@@ -451,8 +457,10 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
           const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + mt * 32 * L::kRowK + 16 * ks);
           sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[ks], sc[mt], 0, 0, 0);
         }
-      // Lane (query column, half) holds rows 8i + 4half + v (register 4i + v).
-      // Only tiles crossing Skv or the causal diagonal need the key test.
+      // Lane (query column, half) holds rows 8i + 4half + v (register 4i +
+      // v).  Scores stay unscaled (the scale's sign is folded into Q, its
+      // magnitude into the exponent); only tiles crossing Skv or the causal
+      // diagonal need the key test.
       const bool edge = kb + kKT > a.Skv || (a.causal && kb + kKT - 1 > q0);
       float mx = -INFINITY;
       if (edge) {
@@ -463,39 +471,51 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
             const int key = kb + mt * 32 + key32_of(8 * (rr >> 2) + 4 * half + (rr & 3));
             bool keep = key < a.Skv;
             if (a.causal) keep = keep && key <= qi;
-            const float x = keep ? sc[mt][rr] * a.scale_log2 : -INFINITY;
-            sc[mt][rr] = x;
-            mx = fmaxf(mx, x);
+            sc[mt][rr] = keep ? sc[mt][rr] : -INFINITY;
+            mx = fmaxf(mx, sc[mt][rr]);
           }
       } else {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int rr = 0; rr < 16; ++rr) {
-            const float x = sc[mt][rr] * a.scale_log2;
-            sc[mt][rr] = x;
-            mx = fmaxf(mx, x);
-          }
+          for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, sc[mt][rr]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_abs;  // log2 domain
+      // Lazy rescale: the running max moves only when a score exceeds it by
+      // more than 2^8, so P <= 256 (fine in fp16) and most steps skip the
+      // rescale of O; O / l is exact whatever max is used.
+#ifdef SPYRE_SDPA_EAGER_RESCALE
+      {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+        m_run = m_new;
+      }
+#else
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+        m_run = m_new;
+      }
+#endif
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
       f16x8 pb[4];
       float psum = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
-          const float p = fast_exp2(sc[mt][rr] - m_use);
+          const float p = fast_exp2(__builtin_fmaf(sc[mt][rr], scale_abs, -m_use));  // masked: exp2(-inf) = 0
           psum += p;
           const int i = rr >> 2;
           pb[mt * 2 + (i >> 1)][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
         }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+      l_run += psum;
       const _Float16* vrow = vt + col * L::kRowV + 8 * half;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
