@@ -45,7 +45,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQ = 32;      // queries per wavefront (two MFMA column tiles)
 constexpr int kKeys = 64;   // keys per step
-constexpr int kStick = 64;  // Vt token padding
+constexpr int kStick = 64;  // Vt token padding (one LDS stage of keys)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -309,16 +309,19 @@ constexpr int kWaves2 = 8;
 constexpr int kThreads2 = kWaves2 * 64;
 constexpr int kQW = 32;             // queries per wavefront
 constexpr int kQB = kWaves2 * kQW;  // queries per workgroup
-constexpr int kKT = 64;             // keys per tile
+constexpr int kKT = 64;             // keys per compute step
+constexpr int kSub = 1;             // compute steps per LDS stage (one barrier each stage)
+constexpr int kKS = kKT * kSub;     // keys per LDS stage
+static_assert(kStick % kKS == 0, "the Vt padding must cover whole stages");
 constexpr int kPadH = 8;            // LDS row padding, halves (16 bytes)
 
 template <int D>
 struct Lds2 {
   static constexpr int kRowK = D + kPadH;    // K tile row (one key), halves
-  static constexpr int kRowV = kKT + kPadH;  // Vt tile row (one feature), halves
-  static constexpr int kK = kKT * kRowK;
+  static constexpr int kRowV = kKS + kPadH;  // Vt tile row (one feature), halves
+  static constexpr int kK = kKS * kRowK;
   static constexpr int kStage = kK + D * kRowV;
-  static constexpr int kChunksK = kKT * D / 8;  // 16-byte chunks per tile
+  static constexpr int kChunksK = kKS * D / 8;  // 16-byte chunks per stage
   static constexpr int kChunks = 2 * kChunksK;  // K and Vt
   static constexpr int kPer = kChunks / kThreads2;
   static_assert(kChunksK % kThreads2 == 0, "K chunks must split evenly over the threads");
@@ -389,9 +392,9 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   const _Float16* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
   const _Float16* vbase = a.vt + b * a.vt_sb + kvh * a.vt_sh;
 
-  // Tile loads: chunk c = thread + kThreads2 * j; chunks [0, kChunksK) are K
-  // rows (keys past Skv read as zeros), the rest Vt rows (zero-padded in the
-  // workspace up to s64, and kb + 64 <= s64).
+  // Stage loads: chunk c = thread + kThreads2 * j; chunks [0, kChunksK) are
+  // K rows (keys past Skv read as zeros), the rest Vt rows (zero-padded in
+  // the workspace up to s64, a multiple of kKS, so kb + kKS <= s64).
   u32x4_t stage_regs[L::kPer];
   auto load_tile = [&](int kb) {
 #pragma unroll
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         stage_regs[j] = key < a.Skv ? *reinterpret_cast<const u32x4_t*>(kbase + key * a.k_ss + c8 * 8)
                                     : u32x4_t{0, 0, 0, 0};
       } else {
-        const int cv = c - L::kChunksK, drow = cv / (kKT / 8), c8 = cv % (kKT / 8);
+        const int cv = c - L::kChunksK, drow = cv / (kKS / 8), c8 = cv % (kKS / 8);
         stage_regs[j] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<int64_t>(drow) * a.s64 + kb + c8 * 8);
       }
     }
@@ -416,14 +419,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         const int row = c / (D / 8), c8 = c % (D / 8);
         *reinterpret_cast<u32x4_t*>(base + row * L::kRowK + c8 * 8) = stage_regs[j];
       } else {
-        const int cv = c - L::kChunksK, drow = cv / (kKT / 8), c8 = cv % (kKT / 8);
+        const int cv = c - L::kChunksK, drow = cv / (kKS / 8), c8 = cv % (kKS / 8);
         *reinterpret_cast<u32x4_t*>(base + L::kK + drow * L::kRowV + c8 * 8) = stage_regs[j];
       }
     }
   };
 
   const int key_end = a.causal ? min(a.Skv, qw0 + kQB) : a.Skv;
-  const int n_tiles = (key_end + kKT - 1) / kKT;
+  const int n_tiles = (key_end + kKS - 1) / kKS;  // LDS stages
   // |scale| (its sign is folded into Q), kept above 0 so that masked scores
   // (-inf) stay -inf; a scale of 0 then gives the uniform weights it should.
   const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
@@ -438,22 +441,26 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   }
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
-    const int kb = t * kKT;
+    const int kb0 = t * kKS;
     const bool more = t + 1 < n_tiles;
-    if (more) load_tile(kb + kKT);  // in flight during this tile's math
-    const _Float16* kt = lds + (t & 1) * L::kStage;
-    const _Float16* vt = kt + L::kK;
-    // Causal: a tile past this wavefront's last query is all masked.
-    const bool active = q0 < a.Sq && (!a.causal || kb <= q0 + kQW - 1);
+    if (more) load_tile(kb0 + kKS);  // in flight during this stage's math
+#pragma unroll
+    for (int sub = 0; sub < kSub; ++sub) {
+    const int kb = kb0 + sub * kKT;
+    const _Float16* kt = lds + (t & 1) * L::kStage + sub * kKT * L::kRowK;
+    const _Float16* vt = lds + (t & 1) * L::kStage + L::kK + sub * kKT;
+    // Past key_end, or (causal) past this wavefront's last query: all masked.
+    const bool active = q0 < a.Sq && kb < key_end && (!a.causal || kb <= q0 + kQW - 1);
     if (active) {
-      // The two key halves' accumulators alternate, so consecutive MFMAs
-      // are independent.
+      // S^T for key halves 0 (keys 0-31) and 1 (32-63), half 0 first: its
+      // softmax then runs on the VALU while half 1's MFMAs are still in the
+      // matrix pipe, and half 1's softmax while half 0's PV MFMAs run.
       f32x16 sc[2] = {f32x16{}, f32x16{}};
       const _Float16* krow = kt + key32_of(col) * L::kRowK + 8 * half;
 #pragma unroll
-      for (int ks = 0; ks < DK; ++ks)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int ks = 0; ks < DK; ++ks) {
           const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + mt * 32 * L::kRowK + 16 * ks);
           sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[ks], sc[mt], 0, 0, 0);
         }
@@ -462,10 +469,11 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       // magnitude into the exponent); only tiles crossing Skv or the causal
       // diagonal need the key test.
       const bool edge = kb + kKT > a.Skv || (a.causal && kb + kKT - 1 > q0);
-      float mx = -INFINITY;
-      if (edge) {
+      const _Float16* vrow = vt + col * L::kRowV + 8 * half;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt) {
+        float mx = -INFINITY;
+        if (edge) {
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr) {
             const int key = kb + mt * 32 + key32_of(8 * (rr >> 2) + 4 * half + (rr & 3));
@@ -474,56 +482,43 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
             sc[mt][rr] = keep ? sc[mt][rr] : -INFINITY;
             mx = fmaxf(mx, sc[mt][rr]);
           }
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        } else {
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, sc[mt][rr]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_abs;  // log2 domain
-      // Lazy rescale: the running max moves only when a score exceeds it by
-      // more than 2^8, so P <= 256 (fine in fp16) and most steps skip the
-      // rescale of O; O / l is exact whatever max is used.
-#ifdef SPYRE_SDPA_EAGER_RESCALE
-      {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-        l_run *= alpha;
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_abs;  // log2 domain
+        // Lazy rescale: the running max moves only when a score exceeds it
+        // by more than 2^8, so P <= 256 (fine in fp16) and most steps skip
+        // the rescale of O; O / l is exact whatever max is used.
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
+          const float m_new = fmaxf(m_run, mx);
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+          l_run *= alpha;
 #pragma unroll
-        for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
-        m_run = m_new;
-      }
-#else
-      if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
-        m_run = m_new;
-      }
-#endif
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      f16x8 pb[4];
-      float psum = 0.f;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+          for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+          m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        f16x8 pb[2];
+        float psum = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
-          const float p = fast_exp2(__builtin_fmaf(sc[mt][rr], scale_abs, -m_use));  // masked: exp2(-inf) = 0
+          const float p = fast_exp2(__builtin_fmaf(sc[mt][rr], scale_abs, -m_use));  // masked: 0
           psum += p;
           const int i = rr >> 2;
-          pb[mt * 2 + (i >> 1)][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
+          pb[i >> 1][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
         }
-      l_run += psum;
-      const _Float16* vrow = vt + col * L::kRowV + 8 * half;
+        l_run += psum;
+        // O^T += Vt[:, keys of this half] P^T: k-steps 2mt, 2mt + 1.
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int dm = 0; dm < DM; ++dm) {
-          const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + dm * 32 * L::kRowV + 16 * ks);
-          o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[ks], o[dm], 0, 0, 0);
-        }
+          for (int dm = 0; dm < DM; ++dm) {
+            const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + dm * 32 * L::kRowV + 16 * (2 * mt + j));
+            o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j], o[dm], 0, 0, 0);
+          }
+      }
+    }
     }
     if (more) store_tile((t + 1) & 1);
     __syncthreads();
