@@ -292,47 +292,64 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(FwdArgs a) {
 // ---- 3. attention with K/V tiles shared through LDS (no mask) -------------
 //
 // One workgroup of kWaves2 wavefronts per 256 queries of one (sequence, q
-// head); wavefront w takes 32 of them.  Each 64-key step, the workgroup
-// stages the K tile [64 keys][D] and the Vt tile [D][64 keys] once in LDS
-// (double-buffered: the next tile's global loads are in flight during this
-// tile's math), and every wavefront reads its MFMA operands from there:
+// head); wavefront w takes 32 of them.  Per 64-key step t the workgroup
+// stages the K tile [64 keys][D] and the Vt tile [D][64 keys] in LDS, and
+// every wavefront reads its MFMA operands from there:
 //   S^T[key, q] = K Q^T   2 x D/16 MFMA 32x32x16 (M = 32 keys, N = 32 queries)
 //   O^T[d, q] += Vt P^T   D/32 x 4 MFMA 32x32x16
-// LDS rows are padded by 16 bytes so that the 16 rows one operand read
-// touches fall in distinct bank groups.  Workgroups are numbered so that
-// those of one (sequence, KV head) run on one XCD (one L2), and for causal
-// attention each head's latest (heaviest) query block starts first.
+// The loop is software-pipelined: K runs one step ahead of V, so while the
+// VALU computes step t's softmax the matrix cores already compute step
+// t+1's scores and then step t's P V.  Two LDS slots each hold K(t+1) /
+// K(t+2) and V(t) / V(t+1); the next tiles' global loads are in flight
+// during a step's math.  LDS rows are padded by 16 bytes so that the rows
+// one operand read touches fall in distinct bank groups.  Workgroups are
+// numbered so that those of one (sequence, KV head) run on one XCD (one L2),
+// and for causal attention each head's latest (heaviest) query block starts
+// first.
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves2 = 8;
 constexpr int kThreads2 = kWaves2 * 64;
 constexpr int kQW = 32;             // queries per wavefront
 constexpr int kQB = kWaves2 * kQW;  // queries per workgroup
-constexpr int kKT = 64;             // keys per compute step
-constexpr int kSub = 1;             // compute steps per LDS stage (one barrier each stage)
-constexpr int kKS = kKT * kSub;     // keys per LDS stage
-static_assert(kStick % kKS == 0, "the Vt padding must cover whole stages");
+constexpr int kKT = 64;             // keys per step
+static_assert(kStick % kKT == 0, "the Vt padding must cover whole steps");
 constexpr int kPadH = 8;            // LDS row padding, halves (16 bytes)
 
 template <int D>
 struct Lds2 {
   static constexpr int kRowK = D + kPadH;    // K tile row (one key), halves
-  static constexpr int kRowV = kKS + kPadH;  // Vt tile row (one feature), halves
-  static constexpr int kK = kKS * kRowK;
-  static constexpr int kStage = kK + D * kRowV;
-  static constexpr int kChunksK = kKS * D / 8;  // 16-byte chunks per stage
-  static constexpr int kChunks = 2 * kChunksK;  // K and Vt
+  static constexpr int kRowV = kKT + kPadH;  // Vt tile row (one feature), halves
+  static constexpr int kK = kKT * kRowK;
+  static constexpr int kSlot = kK + D * kRowV;  // one slot: a K tile and a Vt tile
+  static constexpr int kChunks = kKT * D / 8;   // 16-byte chunks per tile (K or Vt)
   static constexpr int kPer = kChunks / kThreads2;
-  static_assert(kChunksK % kThreads2 == 0, "K chunks must split evenly over the threads");
+  static_assert(kChunks % kThreads2 == 0, "tile chunks must split evenly over the threads");
 };
 
-// Key of row rho of a 32-key S^T tile.  Lane half h (lanes 32h..32h+31)
-// holds rows 8i + 4h + v (i, v < 4); they are the keys 16(i/2) + 8h +
-// 4(i%2) + v, i.e. the two 8-key runs the PV operand of half h needs.
+// S^T row rho of a 32-key half maps to key key32_of(rho) of that half: MFMA
+// row tile i (8 rows) of lane half h holds rows 8i + 4h + v (i, v < 4); they
+// are the keys 16(i/2) + 8h + 4(i%2) + v, i.e. the two 8-key runs the PV
+// operand of half h needs.
 __device__ __forceinline__ int key32_of(int rho) {
   const int i = rho >> 3, h = (rho >> 2) & 1, v = rho & 3;
   return 16 * (i >> 1) + 8 * h + 4 * (i & 1) + v;
+}
+
+// max(x of lane l, x of lane l ^ 32), in every lane.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<unsigned>(r[0])),
+               __builtin_bit_cast(float, static_cast<unsigned>(r[1])));
+}
+
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<unsigned>(r[0])) + __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
 }
 
 struct Fwd2Args {
@@ -355,7 +372,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   using L = Lds2<D>;
   constexpr int DK = D / 16;  // QK k-steps
   constexpr int DM = D / 32;  // O row tiles
-  __shared__ __align__(16) _Float16 lds[2 * L::kStage];
+  __shared__ __align__(16) _Float16 lds[2 * L::kSlot];
 
   // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * g + gi: the
   // blocks of one (sequence, KV head) are consecutive, latest query block
@@ -385,48 +402,61 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       if (a.scale_log2 < 0.f) qv[ks] = -qv[ks];  // the scale's sign, exactly
     }
     // Wait for Q here, outside the loop: otherwise the first MFMA of every
-    // step also waits for the next tile's loads, which are then in flight.
+    // step also waits for the next tiles' loads, which are then in flight.
 #pragma unroll
     for (int ks = 0; ks < DK; ++ks) asm volatile("" : : "v"(qv[ks]));
   }
   const _Float16* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
   const _Float16* vbase = a.vt + b * a.vt_sb + kvh * a.vt_sh;
 
-  // Stage loads: chunk c = thread + kThreads2 * j; chunks [0, kChunksK) are
-  // K rows (keys past Skv read as zeros), the rest Vt rows (zero-padded in
-  // the workspace up to s64, a multiple of kKS, so kb + kKS <= s64).
-  u32x4_t stage_regs[L::kPer];
-  auto load_tile = [&](int kb) {
+  // Tile loads: chunk c = thread + kThreads2 * j, i.e. K row row0 + j * kRowsK
+  // (column c8k) and Vt row drow0 + j * kRowsV (column c8v).  Per-thread
+  // offsets are 32-bit (the host checks that a head spans < 2^31 bytes); the
+  // step's part of the address is uniform.  K rows past Skv read as zeros;
+  // Vt rows are zero-padded in the workspace up to s64, a multiple of kKT,
+  // so kb + kKT <= s64.
+  constexpr int kRowsK = kThreads2 / (D / 8), kRowsV = kThreads2 / (kKT / 8);
+  const int row0 = threadIdx.x / (D / 8), c8k = threadIdx.x % (D / 8);
+  const int drow0 = threadIdx.x / (kKT / 8), c8v = threadIdx.x % (kKT / 8);
+  // (unsigned: for rows past Skv the product may wrap; those rows are not read)
+  const uint32_t koff = static_cast<uint32_t>(row0) * static_cast<uint32_t>(a.k_ss) + c8k * 8;
+  const uint32_t voff = static_cast<uint32_t>(drow0 * a.s64 + c8v * 8);
+  const uint32_t kst = static_cast<uint32_t>(row0 * L::kRowK + c8k * 8);
+  const uint32_t vst = static_cast<uint32_t>(L::kK + drow0 * L::kRowV + c8v * 8);
+  u32x4_t kreg[L::kPer], vreg[L::kPer];
+  auto load_k = [&](int kb) {
+    const _Float16* base = kbase + static_cast<int64_t>(kb) * a.k_ss;
 #pragma unroll
     for (int j = 0; j < L::kPer; ++j) {
-      const int c = threadIdx.x + j * kThreads2;
-      if (j * kThreads2 < L::kChunksK) {
-        const int row = c / (D / 8), c8 = c % (D / 8), key = kb + row;
-        stage_regs[j] = key < a.Skv ? *reinterpret_cast<const u32x4_t*>(kbase + key * a.k_ss + c8 * 8)
-                                    : u32x4_t{0, 0, 0, 0};
-      } else {
-        const int cv = c - L::kChunksK, drow = cv / (kKS / 8), c8 = cv % (kKS / 8);
-        stage_regs[j] = *reinterpret_cast<const u32x4_t*>(vbase + static_cast<int64_t>(drow) * a.s64 + kb + c8 * 8);
-      }
+      const _Float16* p = base + static_cast<int64_t>(j * kRowsK) * a.k_ss;
+      kreg[j] = kb + row0 + j * kRowsK < a.Skv ? *reinterpret_cast<const u32x4_t*>(p + koff) : u32x4_t{0, 0, 0, 0};
     }
   };
-  auto store_tile = [&](int stage) {
-    _Float16* base = lds + stage * L::kStage;
+  auto load_v = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < L::kPer; ++j) {
-      const int c = threadIdx.x + j * kThreads2;
-      if (j * kThreads2 < L::kChunksK) {
-        const int row = c / (D / 8), c8 = c % (D / 8);
-        *reinterpret_cast<u32x4_t*>(base + row * L::kRowK + c8 * 8) = stage_regs[j];
-      } else {
-        const int cv = c - L::kChunksK, drow = cv / (kKS / 8), c8 = cv % (kKS / 8);
-        *reinterpret_cast<u32x4_t*>(base + L::kK + drow * L::kRowV + c8 * 8) = stage_regs[j];
-      }
+      const _Float16* p = vbase + static_cast<int64_t>(j * kRowsV) * a.s64 + kb;
+      vreg[j] = *reinterpret_cast<const u32x4_t*>(p + voff);
     }
+  };
+  auto store_k = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < L::kPer; ++j)
+      *reinterpret_cast<u32x4_t*>(lds + slot * L::kSlot + j * kRowsK * L::kRowK + kst) = kreg[j];
+  };
+  auto store_v = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < L::kPer; ++j)
+      *reinterpret_cast<u32x4_t*>(lds + slot * L::kSlot + j * kRowsV * L::kRowV + vst) = vreg[j];
   };
 
   const int key_end = a.causal ? min(a.Skv, qw0 + kQB) : a.Skv;
-  const int n_tiles = (key_end + kKS - 1) / kKS;  // LDS stages
+  const int n_tiles = (key_end + kKT - 1) / kKT;
+  // Step t has work for this wavefront unless all its keys are masked
+  // (causal: keys past the wavefront's last query).
+  auto active = [&](int t) { return t < n_tiles && q0 < a.Sq && (!a.causal || t * kKT <= q0 + kQW - 1); };
+  // Only steps crossing Skv or the causal diagonal need the key test.
+  auto edge = [&](int t) { return t * kKT + kKT > a.Skv || (a.causal && t * kKT + kKT - 1 > q0); };
   // |scale| (its sign is folded into Q), kept above 0 so that masked scores
   // (-inf) stay -inf; a scale of 0 then gives the uniform weights it should.
   const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
@@ -435,96 +465,138 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 #pragma unroll
   for (int dm = 0; dm < DM; ++dm) o[dm] = f32x16{};
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int t = 0; t < n_tiles; ++t) {
-    const int kb0 = t * kKS;
-    const bool more = t + 1 < n_tiles;
-    if (more) load_tile(kb0 + kKS);  // in flight during this stage's math
+  // S^T half mt (keys 32mt .. 32mt + 31 of the step) from the K tile at kt.
+  auto qk = [&](const _Float16* kt, int mt) {
+    const _Float16* krow = kt + (mt * 32 + key32_of(col)) * L::kRowK + 8 * half;
+    f32x16 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const f16x8*>(krow), qv[0], f32x16{}, 0, 0, 0);
 #pragma unroll
-    for (int sub = 0; sub < kSub; ++sub) {
-    const int kb = kb0 + sub * kKT;
-    const _Float16* kt = lds + (t & 1) * L::kStage + sub * kKT * L::kRowK;
-    const _Float16* vt = lds + (t & 1) * L::kStage + L::kK + sub * kKT;
-    // Past key_end, or (causal) past this wavefront's last query: all masked.
-    const bool active = q0 < a.Sq && kb < key_end && (!a.causal || kb <= q0 + kQW - 1);
-    if (active) {
-      // S^T for key halves 0 (keys 0-31) and 1 (32-63), half 0 first: its
-      // softmax then runs on the VALU while half 1's MFMAs are still in the
-      // matrix pipe, and half 1's softmax while half 0's PV MFMAs run.
-      f32x16 sc[2] = {f32x16{}, f32x16{}};
-      const _Float16* krow = kt + key32_of(col) * L::kRowK + 8 * half;
+    for (int ks = 1; ks < DK; ++ks) {
+      const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + 16 * ks);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[ks], acc, 0, 0, 0);
+    }
+    return acc;
+  };
+  // Lane (query column, half) holds S^T rows 8i + 4half + v of each 32-key
+  // half (register 4i + v).  Masked scores become -inf.
+  const int key_last = a.causal ? min(a.Skv - 1, qi) : a.Skv - 1;  // this lane's last visible key
+  auto mask_step = [&](int t, f32x16 (&s)[2]) {
+    const int kl = key_last - t * kKT - 8 * half;  // key32_of adds 8 per lane half
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int ks = 0; ks < DK; ++ks) {
-          const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + mt * 32 * L::kRowK + 16 * ks);
-          sc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qv[ks], sc[mt], 0, 0, 0);
-        }
-      // Lane (query column, half) holds rows 8i + 4half + v (register 4i +
-      // v).  Scores stay unscaled (the scale's sign is folded into Q, its
-      // magnitude into the exponent); only tiles crossing Skv or the causal
-      // diagonal need the key test.
-      const bool edge = kb + kKT > a.Skv || (a.causal && kb + kKT - 1 > q0);
-      const _Float16* vrow = vt + col * L::kRowV + 8 * half;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        float mx = -INFINITY;
-        if (edge) {
-#pragma unroll
-          for (int rr = 0; rr < 16; ++rr) {
-            const int key = kb + mt * 32 + key32_of(8 * (rr >> 2) + 4 * half + (rr & 3));
-            bool keep = key < a.Skv;
-            if (a.causal) keep = keep && key <= qi;
-            sc[mt][rr] = keep ? sc[mt][rr] : -INFINITY;
-            mx = fmaxf(mx, sc[mt][rr]);
-          }
-        } else {
-#pragma unroll
-          for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, sc[mt][rr]);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_abs;  // log2 domain
-        // Lazy rescale: the running max moves only when a score exceeds it
-        // by more than 2^8, so P <= 256 (fine in fp16) and most steps skip
-        // the rescale of O; O / l is exact whatever max is used.
-        if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
-          const float m_new = fmaxf(m_run, mx);
-          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-          l_run *= alpha;
-#pragma unroll
-          for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
-          m_run = m_new;
-        }
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        f16x8 pb[2];
-        float psum = 0.f;
-#pragma unroll
-        for (int rr = 0; rr < 16; ++rr) {
-          const float p = fast_exp2(__builtin_fmaf(sc[mt][rr], scale_abs, -m_use));  // masked: 0
-          psum += p;
-          const int i = rr >> 2;
-          pb[i >> 1][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
-        }
-        l_run += psum;
-        // O^T += Vt[:, keys of this half] P^T: k-steps 2mt, 2mt + 1.
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int dm = 0; dm < DM; ++dm) {
-            const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + dm * 32 * L::kRowV + 16 * (2 * mt + j));
-            o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j], o[dm], 0, 0, 0);
-          }
+      for (int rr = 0; rr < 16; ++rr) {
+        const int kr = mt * 32 + key32_of(8 * (rr >> 2) + (rr & 3));  // key - t kKT - 8 half
+        s[mt][rr] = kr <= kl ? s[mt][rr] : -INFINITY;
       }
+  };
+  // The running max (log2 domain) moves only when a score of the step
+  // exceeds it by more than 2^8, so P <= 256 (fine in fp16) and most steps
+  // skip the rescale of O; O / l is exact whatever max is used.
+  auto update_max = [&](const f32x16 (&s)[2]) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[mt][rr]);
+    mx = max_xor32(mx) * scale_abs;
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+      m_run = m_new;
     }
+  };
+  // P (fp16) of half mt; the row sum adds the same fp16 values the PV
+  // product uses.
+  auto softmax_half = [&](const f32x16& s, float neg_m, f16x8 (&pb)[2]) {
+    float psum = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const float p = fast_exp2(__builtin_fmaf(s[rr], scale_abs, neg_m));  // masked: 0
+      const int i = rr >> 2;
+      pb[i >> 1][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
     }
-    if (more) store_tile((t + 1) & 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        psum = __builtin_amdgcn_fdot2(f16x2{pb[j][2 * e], pb[j][2 * e + 1]}, f16x2{1, 1}, psum, false);
+    l_run += psum;
+  };
+  // O^T += Vt[:, keys of half mt] P^T: k-steps 2mt, 2mt + 1.
+  auto pv_half = [&](const _Float16* vt, int mt, const f16x8 (&pb)[2]) {
+    const _Float16* vrow = vt + col * L::kRowV + 8 * half;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int dm = 0; dm < DM; ++dm) {
+        const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + dm * 32 * L::kRowV + 16 * (2 * mt + j));
+        o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j], o[dm], 0, 0, 0);
+      }
+  };
+
+  // Step t: LDS holds K(t+1) in slot (t+1)&1 and V(t) in slot t&1, cur
+  // holds S(t), K(t+2) and V(t+1) are in flight; the step leaves S(t+1) in
+  // nxt.  The MFMAs of S(t+1) and of step t's P V overlap step t's softmax:
+  // each scheduling region pairs one MFMA group with one VALU group (and
+  // bounds how far operand reads are hoisted).  At a wavefront's last active
+  // step S(t+1) reads a stale K slot and is never used.
+  auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+    const _Float16* k1 = lds + ((t + 1) & 1) * L::kSlot;
+    const _Float16* vt = lds + (t & 1) * L::kSlot + L::kK;
+    if (active(t)) {
+      if (edge(t)) mask_step(t, cur);
+      nxt[0] = qk(k1, 0);
+      update_max(cur);
+      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+      f16x8 p0[2], p1[2];
+      nxt[1] = qk(k1, 1);
+      softmax_half(cur[0], neg_m, p0);
+      __builtin_amdgcn_sched_barrier(0);
+      pv_half(vt, 0, p0);
+      softmax_half(cur[1], neg_m, p1);
+      __builtin_amdgcn_sched_barrier(0);
+      pv_half(vt, 1, p1);
+    }
+    // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces V(t-1).
+    // The next loads are issued before the barrier: their issue (all
+    // wavefronts at once, 32 KB per workgroup) then overlaps the wait.
+    if (t + 2 < n_tiles) store_k(t & 1);
+    if (t + 1 < n_tiles) store_v((t + 1) & 1);
+    if (t + 3 < n_tiles) load_k((t + 3) * kKT);
+    if (t + 2 < n_tiles) load_v((t + 2) * kKT);
     __syncthreads();
+  };
+
+  // Prologue: K(0), V(0) in slot 0, then S(0), then K(1) in slot 1.  A step
+  // writes nxt only when it is active, and a step is active only if the one
+  // before it is, so S is never read unwritten.
+  f32x16 sa[2], sb[2];
+  if (n_tiles > 0) {
+    load_k(0);
+    load_v(0);
+    store_k(0);
+    store_v(0);
+  }
+  if (n_tiles > 1) load_k(kKT);
+  __syncthreads();
+  if (active(0)) {
+    sa[0] = qk(lds, 0);
+    sa[1] = qk(lds, 1);
+  }
+  if (n_tiles > 1) store_k(1);
+  __syncthreads();
+  if (n_tiles > 2) load_k(2 * kKT);
+  if (n_tiles > 1) load_v(kKT);
+  // Two steps per iteration, S(t) alternating between sa and sb.
+  for (int t = 0; t < n_tiles; t += 2) {
+    step(t, sa, sb);
+    if (t + 1 < n_tiles) step(t + 1, sb, sa);
   }
 
-  float l = l_run + __shfl_xor(l_run, 32, 64);
+  const float l = sum_xor32(l_run);
   if (!q_ok) return;
   _Float16* op = a.out + ((static_cast<int64_t>(b) * a.Sq + qi) * a.Hq + h) * D;
   const float inv = l > 0.f ? 1.f / l : 0.f;
