@@ -48,7 +48,9 @@ def build(verbose: bool = False, out: str = OUT, build_dir: str = BUILD, defines
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
         objs = list(ex.map(lambda f: _compile(f, build_dir, defines), SOURCES))
     tmp = out + ".tmp"
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", *objs, "-o", tmp]
+    # --no-undefined: a kernel whose host stub was not emitted fails here,
+    # not at the first dlopen.
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-Wl,--no-undefined", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

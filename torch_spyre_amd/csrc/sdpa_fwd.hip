@@ -57,6 +57,16 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // part in an SGPR / immediate.  Accesses past the extent read zeros.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit format
+// 16 bytes per lane from buffer offset voff into LDS: lane l writes the 16
+// bytes at dst + 16 l (dst wave-uniform).  Lanes whose offset lies past the
+// buffer's range write zeros.
+__device__ __forceinline__ void load_lds16(Rsrc r, _Float16* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
+// Range of the buffer descriptors whose bases move with the key step; the
+// host keeps every head's K and Vt span within it.
+constexpr uint32_t kBufRange = 0x7ffffff0u;
 
 __device__ __forceinline__ Rsrc make_rsrc(const _Float16* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), 0, bytes, kRsrcWord3);
@@ -409,46 +419,49 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   const _Float16* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
   const _Float16* vbase = a.vt + b * a.vt_sb + kvh * a.vt_sh;
 
-  // Tile loads: chunk c = thread + kThreads2 * j, i.e. K row row0 + j * kRowsK
-  // (column c8k) and Vt row drow0 + j * kRowsV (column c8v).  Per-thread
-  // offsets are 32-bit (the host checks that a head spans < 2^31 bytes); the
-  // step's part of the address is uniform.  K rows past Skv read as zeros;
-  // Vt rows are zero-padded in the workspace up to s64, a multiple of kKT,
-  // so kb + kKT <= s64.
-  constexpr int kRowsK = kThreads2 / (D / 8), kRowsV = kThreads2 / (kKT / 8);
-  const int row0 = threadIdx.x / (D / 8), c8k = threadIdx.x % (D / 8);
-  const int drow0 = threadIdx.x / (kKT / 8), c8v = threadIdx.x % (kKT / 8);
-  // (unsigned: for rows past Skv the product may wrap; those rows are not read)
-  const uint32_t koff = static_cast<uint32_t>(row0) * static_cast<uint32_t>(a.k_ss) + c8k * 8;
-  const uint32_t voff = static_cast<uint32_t>(drow0 * a.s64 + c8v * 8);
-  const uint32_t kst = static_cast<uint32_t>(row0 * L::kRowK + c8k * 8);
-  const uint32_t vst = static_cast<uint32_t>(L::kK + drow0 * L::kRowV + c8v * 8);
-  u32x4_t kreg[L::kPer], vreg[L::kPer];
-  auto load_k = [&](int kb) {
-    const _Float16* base = kbase + static_cast<int64_t>(kb) * a.k_ss;
+  // Tiles move from L2 straight into LDS (buffer loads with the LDS flag):
+  // lane l of a load writes the 16 bytes at M0 + 16 l, so load i of a tile
+  // fills its 16-byte units 64 i .. 64 i + 63, padded rows included.  Lane
+  // l of load i fetches the unit's source; pad units and K rows past Skv get
+  // an offset past the buffer's range and are written as zeros.  Per-lane
+  // offsets are fixed for the whole loop; the step only moves the base.
+  constexpr int kUK = L::kRowK / 8, kUV = L::kRowV / 8;  // 16-byte units per padded row
+  constexpr int kNK = kKT * kUK / 64, kNV = D * kUV / 64;  // loads per tile
+  static_assert(kKT * kUK % 64 == 0 && D * kUV % 64 == 0, "tiles must be whole loads");
+  constexpr int kJK = (kNK + kWaves2 - 1) / kWaves2, kJV = (kNV + kWaves2 - 1) / kWaves2;
+  constexpr uint32_t kOob = 0x80000000u;  // past kBufRange
+  uint32_t k_off[kJK], k_row[kJK], v_off[kJV];
 #pragma unroll
-    for (int j = 0; j < L::kPer; ++j) {
-      const _Float16* p = base + static_cast<int64_t>(j * kRowsK) * a.k_ss;
-      kreg[j] = kb + row0 + j * kRowsK < a.Skv ? *reinterpret_cast<const u32x4_t*>(p + koff) : u32x4_t{0, 0, 0, 0};
-    }
-  };
-  auto load_v = [&](int kb) {
+  for (int j = 0; j < kJK; ++j) {
+    const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUK, ch = u % kUK;
+    const bool pad = ch == kUK - 1;
+    k_row[j] = pad ? kOob : static_cast<uint32_t>(row);
+    k_off[j] = pad ? kOob : (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.k_ss) + 8 * ch) * 2;
+  }
 #pragma unroll
-    for (int j = 0; j < L::kPer; ++j) {
-      const _Float16* p = vbase + static_cast<int64_t>(j * kRowsV) * a.s64 + kb;
-      vreg[j] = *reinterpret_cast<const u32x4_t*>(p + voff);
-    }
-  };
-  auto store_k = [&](int slot) {
+  for (int j = 0; j < kJV; ++j) {
+    const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUV, ch = u % kUV;
+    v_off[j] = ch == kUV - 1 ? kOob : static_cast<uint32_t>(row * a.s64 + 8 * ch) * 2;
+  }
+  // K rows kb .. kb + 63 into slot `slot` (rows >= Skv as zeros).
+  auto dma_k = [&](int kb, int slot) {
+    const Rsrc r = make_rsrc(kbase + static_cast<int64_t>(kb) * a.k_ss, kBufRange);
+    const uint32_t rows_left = static_cast<uint32_t>(a.Skv - kb);
 #pragma unroll
-    for (int j = 0; j < L::kPer; ++j)
-      *reinterpret_cast<u32x4_t*>(lds + slot * L::kSlot + j * kRowsK * L::kRowK + kst) = kreg[j];
+    for (int j = 0; j < kJK; ++j)
+      if (wave + kWaves2 * j < kNK)
+        load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_row[j] < rows_left ? k_off[j] : kOob);
   };
-  auto store_v = [&](int slot) {
+  // Vt columns kb .. kb + 63 (zero-padded up to s64 in the workspace).
+  auto dma_v = [&](int kb, int slot) {
+    const Rsrc r = make_rsrc(vbase + kb, kBufRange);
 #pragma unroll
-    for (int j = 0; j < L::kPer; ++j)
-      *reinterpret_cast<u32x4_t*>(lds + slot * L::kSlot + j * kRowsV * L::kRowV + vst) = vreg[j];
+    for (int j = 0; j < kJV; ++j)
+      if (wave + kWaves2 * j < kNV)
+        load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_off[j]);
   };
+  // The loads must have landed before the barrier that publishes them.
+  auto dma_wait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
   const int key_end = a.causal ? min(a.Skv, qw0 + kQB) : a.Skv;
   const int n_tiles = (key_end + kKT - 1) / kKT;
@@ -538,14 +551,17 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   };
 
   // Step t: LDS holds K(t+1) in slot (t+1)&1 and V(t) in slot t&1, cur
-  // holds S(t), K(t+2) and V(t+1) are in flight; the step leaves S(t+1) in
-  // nxt.  The MFMAs of S(t+1) and of step t's P V overlap step t's softmax:
+  // holds S(t); the step loads K(t+2) and V(t+1) and leaves S(t+1) in nxt.  The MFMAs of S(t+1) and of step t's P V overlap step t's softmax:
   // each scheduling region pairs one MFMA group with one VALU group (and
   // bounds how far operand reads are hoisted).  At a wavefront's last active
   // step S(t+1) reads a stale K slot and is never used.
   auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
     const _Float16* k1 = lds + ((t + 1) & 1) * L::kSlot;
     const _Float16* vt = lds + (t & 1) * L::kSlot + L::kK;
+    // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces V(t-1);
+    // both land during this step's math.
+    if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
+    if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
     if (active(t)) {
       if (edge(t)) mask_step(t, cur);
       nxt[0] = qk(k1, 0);
@@ -560,36 +576,26 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       __builtin_amdgcn_sched_barrier(0);
       pv_half(vt, 1, p1);
     }
-    // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces V(t-1).
-    // The next loads are issued before the barrier: their issue (all
-    // wavefronts at once, 32 KB per workgroup) then overlaps the wait.
-    if (t + 2 < n_tiles) store_k(t & 1);
-    if (t + 1 < n_tiles) store_v((t + 1) & 1);
-    if (t + 3 < n_tiles) load_k((t + 3) * kKT);
-    if (t + 2 < n_tiles) load_v((t + 2) * kKT);
+    dma_wait();
     __syncthreads();
   };
 
-  // Prologue: K(0), V(0) in slot 0, then S(0), then K(1) in slot 1.  A step
+  // Prologue: K(0), V(0) in slot 0 and K(1) in slot 1, then S(0).  A step
   // writes nxt only when it is active, and a step is active only if the one
   // before it is, so S is never read unwritten.
   f32x16 sa[2], sb[2];
   if (n_tiles > 0) {
-    load_k(0);
-    load_v(0);
-    store_k(0);
-    store_v(0);
+    dma_k(0, 0);
+    dma_v(0, 0);
   }
-  if (n_tiles > 1) load_k(kKT);
+  if (n_tiles > 1) dma_k(kKT, 1);
+  dma_wait();
   __syncthreads();
   if (active(0)) {
     sa[0] = qk(lds, 0);
     sa[1] = qk(lds, 1);
   }
-  if (n_tiles > 1) store_k(1);
-  __syncthreads();
-  if (n_tiles > 2) load_k(2 * kKT);
-  if (n_tiles > 1) load_v(kKT);
+  __syncthreads();  // step 0 overwrites K(0)
   // Two steps per iteration, S(t) alternating between sa and sb.
   for (int t = 0; t < n_tiles; t += 2) {
     step(t, sa, sb);
@@ -689,7 +695,7 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
   // Buffer extents (bytes) of one head: K rows 0..Skv-1, Vt [D, s64].
   const int64_t k_span = Skv > 0 ? ((static_cast<int64_t>(Skv) - 1) * k_strides[2] + D) * 2 : 0;
   const int64_t vt_span = static_cast<int64_t>(D) * s64 * 2;
-  SPYRE_REQUIRE(k_span < (int64_t{1} << 31) && vt_span < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
+  SPYRE_REQUIRE(k_span <= kBufRange && vt_span <= kBufRange, SPYRE_EUNSUPPORTED,
                 "one head of K or V spans 2 GiB or more");
   fa.k_bytes = static_cast<uint32_t>(k_span);
   fa.vt_bytes = static_cast<uint32_t>(vt_span);
