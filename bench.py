@@ -14,7 +14,7 @@ serve a step from the previous one.
 Also timed: under "more_configs", the ragged batch (64 sequences, context
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
 heads, append one token at position 131072, attend over 131073 tokens) and
-causal prefill SDPA (batch 1, 32 q / 8 KV heads, 4096 tokens);
+prefill SDPA, causal and full (batch 1, 32 q / 8 KV heads, 4096 tokens);
 under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
 transpose-restick, rotating 8 buffer pairs.
 
@@ -173,19 +173,21 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
         "kernels_per_step": 1 + call.passes}
     del cache, call
 
-    # prefill SDPA: batch 1, 32 q / 8 KV heads, 4096 tokens, causal (MFMA-bound)
+    # prefill SDPA: batch 1, 32 q / 8 KV heads, 4096 tokens, causal and full
+    # (MFMA-bound; flops count the unmasked score pairs only)
     S, PEAK_F16 = 4096, 2.5e15
     q = torch.randn((1, HQ, S, D), generator=gg, device=dev).half()
     k = torch.randn((1, HKV, S, D), generator=gg, device=dev).half()
     v = torch.randn((1, HKV, S, D), generator=gg, device=dev).half()
     ws = torch.empty(tsa.sdpa.workspace_bytes(1, HKV, S, D), dtype=torch.uint8, device=dev)
-    ms = timed(lambda i: tsa.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True, workspace=ws),
-               max(steps // 5, 3), 2, stream)
-    flops = 4 * HQ * D * S * (S + 1) / 2
-    res["prefill_b1_h32_8_s4096_causal"] = {
-        "us_per_step": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
-        "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / PEAK_F16, 4), "flops": flops,
-        "kernels_per_step": 2}
+    for causal in (True, False):
+        ms = timed(lambda i: tsa.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True,
+                                                              workspace=ws), max(steps // 5, 3), 2, stream)
+        flops = 4 * HQ * D * (S * (S + 1) / 2 if causal else S * S)
+        res["prefill_b1_h32_8_s4096" + ("_causal" if causal else "")] = {
+            "us_per_step": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / PEAK_F16, 4), "flops": flops,
+            "kernels_per_step": 2}
     return res
 
 
