@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 
 #include "spyre_common.h"
@@ -131,11 +132,6 @@ __device__ __forceinline__ void shuffle_pair(f16x8& x, f16x8& y, bool bit3) {
   y = op1;
 }
 
-// QK block jh = (j, h): MFMA row i <-> token 32j + 8(i/4) + 4h + i%4.
-__device__ __forceinline__ int qk_token(int jh, int i) {
-  return 32 * (jh >> 1) + 8 * (i >> 2) + 4 * (jh & 1) + (i & 3);
-}
-
 // Pages are read with buffer loads: a resource (base, size) per page in
 // SGPRs, a 32-bit per-lane offset in a VGPR and the load-invariant part of
 // the offset in an SGPR / immediate.  This keeps address registers to four
@@ -149,7 +145,6 @@ __device__ __forceinline__ Rsrc page_rsrc(const _Float16* base, int bytes) {
 }
 
 __device__ __forceinline__ f16x8 bload(Rsrc r, int voff, int soff) {
-  typedef int i32x4 __attribute__((ext_vector_type(4)));
   return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT));
 }
 
@@ -158,7 +153,9 @@ struct LoadOffsets {
   int kx, ky, vx, vy;
   __device__ __forceinline__ explicit LoadOffsets(int lane) {
     const int r = lane & 7, cx = chunk_x(lane), cy = chunk_y(lane);
-    const int tx = 8 * (r >> 2) + (r & 3);  // qk_token(0, r); block jh adds 32j + 4h
+    // QK block jh = (j, h): MFMA row i <-> token 32j + 8(i/4) + 4h + i%4;
+    // this is block 0's token of row r.
+    const int tx = 8 * (r >> 2) + (r & 3);
     kx = (tx * 64 + cx * 8) * 2;
     ky = ((tx + 16) * 64 + cy * 8) * 2;     // row 8 + r is token tx + 16
     vx = (r * kPage + cx * 8) * 2;
@@ -571,6 +568,52 @@ extern "C" size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv
 
 namespace {
 
+// Split-kernel workgroups that run at once on the current device (CUs times
+// workgroups per CU), cached per device; 0 if the runtime cannot say.
+int split_slots(int D) {
+  static std::atomic<int> cache[64][2];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::atomic<int>& c = cache[dev][D == 128];
+  int v = c.load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  const hipError_t e =
+      D == 128 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_list_kernel<128>, kThreads, 0)
+               : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_list_kernel<64>, kThreads, 0);
+  if (e != hipSuccess || cus <= 0 || per_cu <= 0) return 0;
+  v = cus * per_cu;
+  c.store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// Pages per chunk.  The requested size cp0 (kWaves x split) may grow by up
+// to a quarter when that packs the workgroups of max_context_len-long
+// sequences into fewer rounds of the device's slots (cost = rounds x pages
+// per chunk); larger chunks never need more workspace than cp0's.  Depends
+// only on the call's sizes and the device, so the two passes of a two-pass
+// call agree.
+int balanced_chunk_pages(int64_t pairs, int max_ctx, int cp0, int slots) {
+  const int64_t n = pages_of(max_ctx);
+  if (slots <= 0 || n <= cp0) return cp0;
+  auto cost = [&](int cp) {
+    const int64_t nch = (n + cp - 1) / cp;
+    const int64_t per = (n + nch - 1) / nch;  // pages of the largest chunk (equal shares)
+    return (pairs * nch + slots - 1) / slots * per;
+  };
+  int best = cp0;
+  int64_t best_cost = cost(cp0);
+  for (int cp = cp0 + 1; cp <= cp0 + cp0 / 4; ++cp) {
+    const int64_t c = cost(cp);
+    if (c < best_cost) {
+      best = cp;
+      best_cost = c;
+    }
+  }
+  return best;
+}
+
 struct Plan {
   SplitArgs sa;
   MergeArgs ma;
@@ -614,7 +657,8 @@ int plan_attn(const void* q, const void* k_cache, const void* v_cache, const int
   SPYRE_REQUIRE(items < (int64_t{1} << 31) && Hkv <= 65535 && B <= 65535,
                 SPYRE_EUNSUPPORTED, "too many work items (B=%d Hkv=%d chunks=%lld)", B, Hkv,
                 static_cast<long long>(max_chunks));
-  const int chunk_pages = kWaves * (split_tokens / kPage);
+  const int chunk_pages = balanced_chunk_pages(static_cast<int64_t>(B) * Hkv, max_context_len,
+                                               kWaves * (split_tokens / kPage), split_slots(D));
   p.sa = SplitArgs{static_cast<const _Float16*>(q), static_cast<const _Float16*>(k_cache),
                    static_cast<const _Float16*>(v_cache), block_table, bt_stride, context_lens,
                    static_cast<float*>(workspace), static_cast<_Float16*>(out), lse, num_pages, B,
