@@ -157,9 +157,11 @@ size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv, int D, in
  *   context_lens : int32 [B]; every context_lens[b] <= max_context_len
  *   lse          : optional fp32 [B, Hq] natural-log logsumexp (NULL to skip)
  * D in {64, 128}, page_size 64, g <= 16, split_tokens a multiple of 64.
- * Each wavefront streams at most split_tokens tokens; a workgroup of 8
- * covers a chunk of up to 8 * split_tokens.  When max_context_len fits one
- * chunk this is one kernel and the workspace is not touched; otherwise the
+ * Each wavefront streams about split_tokens tokens; a workgroup of 8 covers
+ * a chunk of 8 * split_tokens, or up to a quarter more when larger chunks
+ * pack the device's workgroups into fewer rounds (never more chunks than
+ * the workspace formula counts).  When max_context_len <= 8 * split_tokens
+ * this is one kernel and the workspace is not touched; otherwise the
  * chunks' partials are merged by a second kernel.
  * Empty contexts give zeros (as torch's CPU SDPA does).  Replaces the SDPA
  * overrideable decomposition (torch_spyre/_inductor/decompositions.py:523-609)
