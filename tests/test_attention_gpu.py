@@ -286,3 +286,35 @@ def test_workspace_reuse_across_shapes(cuda):
         fresh = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=128,
                                            max_context_len=max(lens))
         assert torch.equal(reused.view(torch.int16), fresh.view(torch.int16)), i
+
+
+def test_balanced_chunks_fill_rounds(cuda):
+    """32 sequences x 8 KV heads of 9 pages at split 64 (8-page chunks): two
+    chunks per (sequence, KV head) would make 512 split workgroups, two rounds
+    on a 256-slot device (256 CUs, one 8-wavefront workgroup each), so the
+    planner grows the chunk to 9 pages and every pair is one chunk.  All rows
+    against the oracle; the two-pass API (whose merge then finds only single
+    chunks) gives the same bits; and on a 256-CU device the result equals
+    split 512 bit for bit (both cut each context into one chunk the same way)."""
+    import torch_spyre_amd as tsa
+
+    B, Hq, Hkv, D = 32, 32, 8, 128
+    lens = [576] * B
+    lens[3], lens[17], lens[31] = 513, 100, 0
+    cache, table, lens_t, q = make_case(cuda, B, Hq, Hkv, D, lens, SEED + 81)
+    t, l = table.to(cuda), lens_t.to(cuda)
+    out, lse = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=64, max_context_len=576,
+                                          return_lse=True)
+    rows = [b for b in range(B) if lens[b] > 0]
+    assert_close(out[rows], oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(D)))
+    assert torch.count_nonzero(out[31]) == 0
+    ws = torch.empty(tsa.workspace_bytes(B, Hq, Hkv, D, 576, 64), dtype=torch.uint8, device=cuda)
+    tsa.paged_decode_split(q, cache.k, cache.v, t, l, ws, split_tokens=64, max_context_len=576)
+    two = torch.empty_like(q)
+    lse2 = torch.empty((B, Hq), dtype=torch.float32, device=cuda)
+    tsa.paged_decode_merge(l, ws, two, Hkv, 576, split_tokens=64, lse=lse2)
+    assert torch.equal(out.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(lse, lse2)
+    if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
+        wide = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=512, max_context_len=576)
+        assert torch.equal(out.view(torch.int16), wide.view(torch.int16))
