@@ -11,12 +11,14 @@ call is one kernel).  Inputs are resident in HBM before the timed region;
 two KV caches (1.07 GB) alternate so the 256 MB last-level cache cannot
 serve a step from the previous one.
 
-Also timed: under "more_configs", the ragged batch (64 sequences, context
+Also timed: under "more_configs", the dense MHA decode call (q [1, 8, 1, 64], k/v
+[1, 8, 512, 64]; absolute µs, launch-bound), the ragged batch (64 sequences, context
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
 heads, append one token at position 131072, attend over 131073 tokens) and
 prefill SDPA, causal and full (batch 1, 32 q / 8 KV heads, 4096 tokens);
 under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
-transpose-restick, rotating 8 buffer pairs.
+transpose-restick, rotating 9 buffer pairs (576 MiB), with torch's CPU
+view/permute/contiguous of the same closed forms as its CPU baseline.
 
 Timing: HIP events on the stream the kernels are launched on, around K
 back-to-back steps, after W warm-up steps.  GB/s = algorithmic bytes / time.
@@ -114,6 +116,35 @@ def cpu_baseline(k_log_pages, v_log_pages, table, q, budget_s=12.0):
     }
 
 
+def cpu_relayout_baseline(x, budget_s=1.0):
+    """The relayout closed forms (to sticks: x.view(R, C/64, 64).permute(1, 0, 2); from sticks:
+    the inverse; transpose-restick: x.view(R/64, 64, C).permute(0, 2, 1)) made contiguous by torch
+    on the host cores, each repeated for about budget_s."""
+    import torch
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    R, C = x.shape
+    sticks = x.view(R, C // 64, 64).permute(1, 0, 2).contiguous()
+    ops = {
+        "to_sticks": lambda: x.view(R, C // 64, 64).permute(1, 0, 2).contiguous(),
+        "from_sticks": lambda: sticks.permute(1, 0, 2).reshape(R, C).contiguous(),
+        "transpose_restick": lambda: x.view(R // 64, 64, C).permute(0, 2, 1).contiguous(),
+    }
+    res = {}
+    nbytes = 2 * x.numel() * x.element_size()
+    for name, fn in ops.items():
+        n, t0 = 0, time.perf_counter()
+        while n < 3 or time.perf_counter() - t0 < budget_s:
+            fn()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res[name] = {"us": round(dt * 1e6, 1), "GB/s": round(nbytes / dt / 1e9, 2)}
+    res["cores"] = torch.get_num_threads()
+    res["kind"] = "port"
+    res["sample"] = f"fp16 [{R}, {C}] bit patterns, each op repeated for ~{budget_s:.0f} s; cpu={cpu_model()}"
+    return res
+
+
 def more_configs(tsa, dev, stream, steps, warmup, seed):
     """The ragged batch and the long-context append + attend step, timed the
     same way (one cache each: both are far larger than the last-level
@@ -123,6 +154,15 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     res = {}
     g = torch.Generator().manual_seed(seed)
     gg = torch.Generator(device=dev).manual_seed(seed + 1)
+
+    # dense MHA decode: q [1, 8, 1, 64], k/v [1, 8, 512, 64], scale 1/8 (launch-bound:
+    # absolute µs; the call relays K/V into pages, then runs the paged kernel)
+    q1 = torch.randn((1, 8, 1, 64), generator=gg, device=dev).half()
+    k1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
+    v1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
+    ms = timed(lambda i: tsa.sdpa_decode(q1, k1, v1, scale=0.125), steps, warmup, stream)
+    res["dense_mha_decode_b1_h8_s512_d64"] = {"us_per_call": round(ms * 1e3, 2),
+                                               "algorithmic_bytes": 1_050_624}
 
     def paged(lens, Hq, Hkv):
         pages = [(c + PAGE - 1) // PAGE for c in lens]
@@ -247,9 +287,17 @@ def main():
 
     # ---------------- relayout (config: [4096, 4096] fp16) ----------------
     R = C = 4096
-    nbuf = 8
-    xs = [torch.randint(-30000, 30000, (R, C), device=dev, dtype=torch.int16).view(torch.float16)
-          for _ in range(nbuf)]
+    nbuf = 9  # 9 x (32 MiB in + 32 MiB out) > 512 MiB: a step's buffers are out of the 256 MB MALL
+
+    def bits16(i):
+        """Random 16-bit patterns; NaN/Inf exponents (0x7C00 all set) get their top exponent bit
+        cleared."""
+        u = torch.randint(0, 1 << 16, (R, C), device=dev, dtype=torch.int32,
+                          generator=torch.Generator(device=dev).manual_seed(seed + 100 + i))
+        u = torch.where((u & 0x7C00) == 0x7C00, u ^ 0x4000, u)
+        return u.to(torch.int16).view(torch.float16)
+
+    xs = [bits16(i) for i in range(nbuf)]
     dflt = tsa.SpyreTensorLayout([R, C], torch.float16)
     trl = tsa.transpose_restick_layout(R, C)
     devs = [tsa.to_device_layout(x, dflt) for x in xs]
@@ -305,6 +353,7 @@ def main():
 
         k_log, v_log = OA.pages_to_logical(c.k.cpu().numpy(), c.v.cpu().numpy(), n_pages, HKV, D)
         result["cpu_baseline"] = cpu_baseline(k_log, v_log, tables[0].cpu().numpy(), q.cpu())
+        result["relayout"]["cpu_baseline"] = cpu_relayout_baseline(xs[0].cpu())
     print(json.dumps(result), flush=True)
 
 

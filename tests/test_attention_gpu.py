@@ -93,6 +93,24 @@ def test_config1_dense_mha_vs_cpu_sdpa(cuda):
     assert_close(out, ref64)
 
 
+@pytest.mark.parametrize("S", [1, 65, 513])
+@pytest.mark.parametrize("D", [64, 128])
+def test_dense_to_pages_then_paged_decode(cuda, S, D):
+    """Dense K/V moved into the page layouts by dense_to_pages (one relayout
+    pass per tensor, tokens past S zero-filled), then the paged kernel."""
+    import torch_spyre_amd as tsa
+
+    g = torch.Generator().manual_seed(SEED + 7 * S + D)
+    q = torch.randn((2, 8, 1, D), generator=g).half()
+    k = torch.randn((2, 2, S, D), generator=g).half()
+    v = torch.randn((2, 2, S, D), generator=g).half()
+    cache, table = tsa.dense_to_pages(k.to(cuda), v.to(cuda))
+    lens = torch.full((2,), S, dtype=torch.int32, device=cuda)
+    out = tsa.paged_decode_attention(q[:, :, 0].contiguous().to(cuda), cache.k, cache.v, table, lens,
+                                     max_context_len=S)
+    assert_close(out.unsqueeze(2), OA.sdpa_cpu_fp32(q, k, v))
+
+
 @pytest.mark.parametrize("S", [1, 63, 64, 65, 200, 513])
 @pytest.mark.parametrize("D", [64, 128])
 def test_dense_gqa_ragged_lengths(cuda, S, D):

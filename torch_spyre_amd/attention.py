@@ -308,12 +308,15 @@ def dense_to_pages(k: torch.Tensor, v: torch.Tensor) -> tuple[PagedKVCache, torc
 
 
 def sdpa_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                scale: Optional[float] = None, enable_gqa: bool = False,
-                split_tokens: int = 512) -> torch.Tensor:
+                scale: Optional[float] = None, enable_gqa: bool = False) -> torch.Tensor:
     """F.scaled_dot_product_attention for one query token (Sq == 1), no mask,
     no dropout: query [B, Hq, 1, D], key/value [B, Hkv, S, D] fp16 ->
-    [B, Hq, 1, D].  Dense K/V are relaid into pages first (as the reference's
-    compiler restickifies K^T for its SDPA), then the paged kernel runs."""
+    [B, Hq, 1, D].  The reference serves decode through the same overrideable
+    SDPA op as prefill (torch_spyre/_inductor/decompositions.py:523-609), and
+    so does this: the SDPA forward kernels with Sq = 1.  Paged caches use
+    ``paged_decode_attention``."""
+    from .sdpa import scaled_dot_product_attention
+
     if query.dim() != 4 or query.shape[2] != 1:
         raise ValueError("sdpa_decode handles exactly one query token: query [B, Hq, 1, D]")
     B, Hq, _, D = query.shape
@@ -322,8 +325,5 @@ def sdpa_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
         raise ValueError("key/value must be [B, Hkv, S, D] matching query")
     if Hq != Hkv and not enable_gqa:
         raise ValueError("Hq != Hkv requires enable_gqa=True")
-    cache, table = dense_to_pages(key.to(torch.float16), value.to(torch.float16))
-    lens = torch.full((B,), S, dtype=torch.int32, device=query.device)
-    out = paged_decode_attention(query[:, :, 0, :].to(torch.float16).contiguous(), cache.k, cache.v,
-                                 table, lens, scale=scale, split_tokens=split_tokens, max_context_len=S)
-    return out.unsqueeze(2)
+    return scaled_dot_product_attention(query.to(torch.float16), key.to(torch.float16), value.to(torch.float16),
+                                        scale=scale, enable_gqa=enable_gqa)
