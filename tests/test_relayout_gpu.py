@@ -203,6 +203,30 @@ def test_transpose_restick_partial_tiles_vs_oracle(cuda, sizes):
     assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
 
 
+@pytest.mark.parametrize("sizes", [[64, 1024], [192, 2048], [2, 128, 1024], [4, 64, 3072]], ids=str)
+def test_transpose_whole_tile_rows_vs_oracle(cuda, sizes):
+    """Transpose nests of whole rows of 64 x 64 tiles with outer loops:
+    device restickify and host -> transposed sticks directly, bit-exact, and
+    back."""
+    import torch_spyre_amd as tsa
+
+    order = list(range(len(sizes)))
+    order[-2], order[-1] = order[-1], order[-2]
+    strides = OL.contiguous_strides(sizes)
+    src = tsa.SpyreTensorLayout(sizes, torch.float16)
+    dst = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + 13 * sum(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    want = OL.h2d(bits, sizes, strides, 0, OL.stl_init(sizes, strides, "float16", order))
+    out = tsa.restickify(tsa.to_device_layout(x, src), dst)
+    out2 = tsa.to_device_layout(x, dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
+    assert np.array_equal(_as_bits(out2).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(out)
+    assert np.array_equal(_as_bits(back).reshape(-1), bits)
+
+
 def test_page_layouts_vs_oracle(cuda):
     """The paged K/V cache layouts built by the relayout engine equal the
     oracle's H2D of the same logical pages."""
