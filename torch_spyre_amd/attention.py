@@ -201,7 +201,9 @@ class PagedDecode:
     alive and keep their storage).  ``__call__`` is the single-call entry
     (one kernel when max_context_len fits one chunk); ``split()`` and
     ``merge()`` launch the two passes separately (the split pass then
-    writes every chunk's partial to the workspace)."""
+    writes every chunk's partial to the workspace).  Each launch goes to the
+    stream current at that moment, so the calls can be captured into a HIP
+    graph (the library allocates and clears nothing)."""
 
     def __init__(self, q, k_cache, v_cache, block_table, context_lens, scale=None,
                  split_tokens: int = 512, max_context_len: Optional[int] = None, workspace=None,
@@ -221,26 +223,28 @@ class PagedDecode:
         self._split_fn = L.spyre_paged_decode_attn_split_f16
         self._merge_fn = L.spyre_paged_decode_attn_merge_f16
         lse_ptr = lse.data_ptr() if lse is not None else None
+        self._device = q.device
         self._call_args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
                            block_table.stride(0), context_lens.data_ptr(), self.out.data_ptr(), lse_ptr,
                            a.ws.data_ptr(), a.ws_bytes, a.B, a.Hq, a.Hkv, a.D, PAGE, a.num_pages,
-                           a.max_ctx, a.split, a.scale, a.stream)
+                           a.max_ctx, a.split, a.scale)
         self._split_args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
                             block_table.stride(0), context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes,
-                            a.B, a.Hq, a.Hkv, a.D, PAGE, a.num_pages, a.max_ctx, a.split, a.scale,
-                            a.stream)
+                            a.B, a.Hq, a.Hkv, a.D, PAGE, a.num_pages, a.max_ctx, a.split, a.scale)
         self._merge_args = (context_lens.data_ptr(), a.ws.data_ptr(), a.ws_bytes, self.out.data_ptr(),
-                            lse_ptr, a.B, a.Hq, a.Hkv, a.D, a.max_ctx, a.split, a.stream)
+                            lse_ptr, a.B, a.Hq, a.Hkv, a.D, a.max_ctx, a.split)
 
     def split(self) -> None:
-        _lib.check("spyre_paged_decode_attn_split_f16", self._split_fn(*self._split_args))
+        _lib.check("spyre_paged_decode_attn_split_f16",
+                   self._split_fn(*self._split_args, _stream_ptr(self._device)))
 
     def merge(self) -> torch.Tensor:
-        _lib.check("spyre_paged_decode_attn_merge_f16", self._merge_fn(*self._merge_args))
+        _lib.check("spyre_paged_decode_attn_merge_f16",
+                   self._merge_fn(*self._merge_args, _stream_ptr(self._device)))
         return self.out
 
     def __call__(self) -> torch.Tensor:
-        _lib.check("spyre_paged_decode_attn_f16", self._call_fn(*self._call_args))
+        _lib.check("spyre_paged_decode_attn_f16", self._call_fn(*self._call_args, _stream_ptr(self._device)))
         return self.out
 
 

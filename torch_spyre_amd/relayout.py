@@ -62,18 +62,21 @@ def dma_copy(src: torch.Tensor, dst: torch.Tensor, infos, elem_bytes: Optional[i
 class DmaCopy:
     """A validated ``dma_copy`` that can be launched repeatedly: the loop-nest
     array and the pointers are built once, each call only enters the library
-    (the tensors must stay alive and keep their storage)."""
+    (the tensors must stay alive and keep their storage).  Each call launches
+    on the stream current at that moment, so calls can be captured into a
+    HIP graph."""
 
     def __init__(self, src: torch.Tensor, dst: torch.Tensor, infos, elem_bytes: Optional[int] = None):
         esz = elem_bytes or src.element_size()
         sp, sb = _storage_span(src)
         dp, db = _storage_span(dst)
         self._infos = (_lib.StrideInfo * max(1, len(infos)))(*infos)
-        self._args = (sp, sb, dp, db, esz, self._infos, len(infos), _stream_ptr(dst.device))
+        self._args = (sp, sb, dp, db, esz, self._infos, len(infos))
+        self._device = dst.device
         self._fn = _lib.lib().spyre_dma_copy
 
     def __call__(self) -> None:
-        _lib.check("spyre_dma_copy", self._fn(*self._args))
+        _lib.check("spyre_dma_copy", self._fn(*self._args, _stream_ptr(self._device)))
 
 
 def _tag(t: torch.Tensor, layout: SpyreTensorLayout, size, stride) -> torch.Tensor:
