@@ -157,6 +157,18 @@ def test_zero_and_negative_scale(cuda, scale, causal):
                  OA.sdpa_cpu_fp32(q, k, v, scale=scale, is_causal=causal))
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_large_scale(cuda, causal):
+    """|scale log2 e| > 1 (here scale 2): Q is not prescaled (q * scale could
+    leave fp16), the scale goes into the exponent instead; nearly one-hot
+    rows."""
+    q, k, v = randn((1, 4, 130, 128), SEED + 43), randn((1, 4, 150, 128), SEED + 44), randn((1, 4, 150, 128), SEED + 45)
+    out, lse = run(cuda, q, k, v, scale=2.0, is_causal=causal, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, scale=2.0, is_causal=causal))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, scale=2.0, is_causal=causal, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=1e-5)
+
+
 def test_unaligned_views_are_accepted(cuda):
     """A head-dim slice of a wider tensor (rows not 16-byte multiples apart)
     is copied into kernel form first; the result is unchanged."""

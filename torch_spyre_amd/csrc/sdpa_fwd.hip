@@ -377,7 +377,12 @@ struct Fwd2Args {
   float scale_log2;
 };
 
-template <int D>
+// PRESCALED (|scale log2 e| <= 1, so q * that never overflows fp16): Q is
+// multiplied by scale log2 e once, and every step's scores leave the MFMA
+// already as exponents: the first QK MFMA starts from a tile holding -m
+// (the running max), so P = exp2(S) needs no per-score FMA.  Otherwise the
+// scale's sign is folded into Q and its magnitude into the exponent's FMA.
+template <int D, bool PRESCALED>
 __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   using L = Lds2<D>;
   constexpr int DK = D / 16;  // QK k-steps
@@ -397,6 +402,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   const int b = static_cast<int>(r / a.Hkv);
   const int h = kvh * a.g + gi;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  __builtin_assume(wave >= 0 && wave < kWaves2);  // lets the compiler drop always-true load guards
   const int qw0 = qb * kQB, q0 = qw0 + wave * kQW;
   const int col = lane & 31, half = lane >> 5;
   const int qi = q0 + col;
@@ -409,7 +415,12 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 #pragma unroll
     for (int ks = 0; ks < DK; ++ks) {
       qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
-      if (a.scale_log2 < 0.f) qv[ks] = -qv[ks];  // the scale's sign, exactly
+      if constexpr (PRESCALED) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[ks][e] = static_cast<_Float16>(static_cast<float>(qv[ks][e]) * a.scale_log2);
+      } else if (a.scale_log2 < 0.f) {
+        qv[ks] = -qv[ks];  // the scale's sign, exactly
+      }
     }
     // Wait for Q here, outside the loop: otherwise the first MFMA of every
     // step also waits for the next tiles' loads, which are then in flight.
@@ -474,6 +485,10 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // (-inf) stay -inf; a scale of 0 then gives the uniform weights it should.
   const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
   float m_run = -INFINITY, l_run = 0.f;
+  // PRESCALED: scores are carried relative to m_use (m_run, or 0 while no
+  // finite score has been seen); neg_m_tile holds -m_use in every row.
+  float m_use = 0.f;
+  f32x16 neg_m_tile = f32x16{};
   f32x16 o[DM];
 #pragma unroll
   for (int dm = 0; dm < DM; ++dm) o[dm] = f32x16{};
@@ -481,7 +496,8 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // S^T half mt (keys 32mt .. 32mt + 31 of the step) from the K tile at kt.
   auto qk = [&](const _Float16* kt, int mt) {
     const _Float16* krow = kt + (mt * 32 + key32_of(col)) * L::kRowK + 8 * half;
-    f32x16 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const f16x8*>(krow), qv[0], f32x16{}, 0, 0, 0);
+    f32x16 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const f16x8*>(krow), qv[0],
+                                                        PRESCALED ? neg_m_tile : f32x16{}, 0, 0, 0);
 #pragma unroll
     for (int ks = 1; ks < DK; ++ks) {
       const f16x8 ka = *reinterpret_cast<const f16x8*>(krow + 16 * ks);
@@ -505,13 +521,16 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // The running max (log2 domain) moves only when a score of the step
   // exceeds it by more than 2^8, so P <= 256 (fine in fp16) and most steps
   // skip the rescale of O; O / l is exact whatever max is used.
-  auto update_max = [&](const f32x16 (&s)[2]) {
+  // PRESCALED: s holds exponents relative to m_use, and so does `ahead`
+  // (the first half of the next step's scores, computed before this
+  // update); a move of m_use shifts both, and the tile.
+  auto update_max = [&](f32x16 (&s)[2], f32x16& ahead) {
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[mt][rr]);
-    mx = max_xor32(mx) * scale_abs;
+    mx = PRESCALED ? max_xor32(mx) + m_use : max_xor32(mx) * scale_abs;
     if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
@@ -519,6 +538,18 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 #pragma unroll
       for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
       m_run = m_new;
+      if constexpr (PRESCALED) {
+        const float m_use_new = m_new == -INFINITY ? m_use : m_new;  // lanes still without a score keep 0
+        const float d = m_use_new - m_use;
+        m_use = m_use_new;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+          s[0][rr] -= d;
+          s[1][rr] -= d;
+          ahead[rr] -= d;
+          neg_m_tile[rr] = -m_use;
+        }
+      }
     }
   };
   // P (fp16) of half mt; the row sum adds the same fp16 values the PV
@@ -527,7 +558,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     float psum = 0.f;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
-      const float p = fast_exp2(__builtin_fmaf(s[rr], scale_abs, neg_m));  // masked: 0
+      const float p = fast_exp2(PRESCALED ? s[rr] : __builtin_fmaf(s[rr], scale_abs, neg_m));  // masked: 0
       const int i = rr >> 2;
       pb[i >> 1][(i & 1) * 4 + (rr & 3)] = static_cast<_Float16>(p);
     }
@@ -565,7 +596,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     if (active(t)) {
       if (edge(t)) mask_step(t, cur);
       nxt[0] = qk(k1, 0);
-      update_max(cur);
+      update_max(cur, nxt[0]);
       const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
       f16x8 p0[2], p1[2];
       nxt[1] = qk(k1, 1);
@@ -748,10 +779,16 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.n_items = static_cast<uint32_t>(items);
     f2.xcd_remap = items % 8 == 0;
     f2.scale_log2 = fa.scale_log2;
-    if (D == 128)
-      sdpa_fwd_lds_kernel<128><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+    // |scale log2 e| <= 1: q times it stays within fp16, so Q is prescaled.
+    const bool prescaled = fabsf(f2.scale_log2) <= 1.f;
+    if (D == 128 && prescaled)
+      sdpa_fwd_lds_kernel<128, true><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+    else if (D == 128)
+      sdpa_fwd_lds_kernel<128, false><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+    else if (prescaled)
+      sdpa_fwd_lds_kernel<64, true><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
     else
-      sdpa_fwd_lds_kernel<64><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+      sdpa_fwd_lds_kernel<64, false><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
   } else {
     const dim3 grid((Sq + kWaves * kQ - 1) / (kWaves * kQ), Hq, B);
     auto launch = [&](auto mk) {
