@@ -218,3 +218,27 @@ def test_llama3_8b_prefill_1024_causal_sampled_heads(cuda):
     for h in (0, 3, 17, 31):
         ref = OA.sdpa_cpu_fp32(q[:, h:h + 1], k[:, h // 4:h // 4 + 1], v[:, h // 4:h // 4 + 1], is_causal=True)
         assert_close(out[:, h:h + 1], ref)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bench_shape_prefill_sampled_heads(cuda, causal):
+    """The measured prefill shape (batch 1, 32 q / 8 KV heads, 4096 tokens,
+    D 128): three q heads from different KV groups against the oracle, LSE of
+    one head against the fp64 logsumexp, and for causal attention the closed
+    form of row 0 (it sees key 0 only: out = v[0]) on every head."""
+    S = 4096
+    q = randn((1, 32, S, 128), SEED + 50)
+    k = randn((1, 8, S, 128), SEED + 51)
+    v = randn((1, 8, S, 128), SEED + 52)
+    out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
+    out, lse = out.cpu(), lse.cpu()
+    for h in (0, 13, 31):
+        kv = h // 4
+        ref = OA.sdpa_cpu_fp32(q[:, h:h + 1], k[:, kv:kv + 1], v[:, kv:kv + 1], is_causal=causal)
+        assert_close(out[:, h:h + 1], ref)
+    _, lse64 = OA.sdpa_decomposition_fp64(q[:, 13:14], k[:, 3:4], v[:, 3:4], is_causal=causal, return_lse=True)
+    assert np.allclose(lse[:, 13:14].numpy(), lse64, atol=LSE_ATOL, rtol=1e-5)
+    if causal:
+        first = out[0, :, 0].float()
+        want = v[0, torch.arange(32) // 4, 0].float()
+        assert torch.equal(first, want)
