@@ -179,7 +179,7 @@ __device__ __forceinline__ void stick_tile(const char* sp, char* dp, int64_t a_s
   u32x4 x[kTileSticks];
 #pragma unroll
   for (int k = 0; k < kTileSticks; ++k, sp += a_ss)
-    if (!GUARDED || (b_lane && k < a_left)) x[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sp));
+    if (!GUARDED || (b_lane && static_cast<uint32_t>(k) < a_left)) x[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sp));
 #pragma unroll
   for (int k = 0; k < kTileSticks; ++k) lds[stick * kRow + k * 8 + unit] = x[k];
   __syncthreads();
@@ -187,7 +187,7 @@ __device__ __forceinline__ void stick_tile(const char* sp, char* dp, int64_t a_s
   for (int k = 0; k < kTileSticks; ++k) x[k] = lds[k * kRow + threadIdx.x];
 #pragma unroll
   for (int k = 0; k < kTileSticks; ++k, dp += b_sd)
-    if (!GUARDED || (a_lane && k < b_left)) __builtin_nontemporal_store(x[k], reinterpret_cast<u32x4*>(dp));
+    if (!GUARDED || (a_lane && static_cast<uint32_t>(k) < b_left)) __builtin_nontemporal_store(x[k], reinterpret_cast<u32x4*>(dp));
 }
 
 __global__ __launch_bounds__(kThreads) void dma_stick_tile_kernel(const char* __restrict__ src,

@@ -45,7 +45,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQ = 32;      // queries per wavefront (two MFMA column tiles)
 constexpr int kKeys = 64;   // keys per step
-constexpr int kStick = 64;  // Vt token padding (one LDS stage of keys)
+constexpr int kStick = 64;  // Vt token padding: whole 64-key steps
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -310,8 +310,8 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(FwdArgs a) {
 // The loop is software-pipelined: K runs one step ahead of V, so while the
 // VALU computes step t's softmax the matrix cores already compute step
 // t+1's scores and then step t's P V.  Two LDS slots each hold K(t+1) /
-// K(t+2) and V(t) / V(t+1); the next tiles' global loads are in flight
-// during a step's math.  LDS rows are padded by 16 bytes so that the rows
+// K(t+2) and V(t) / V(t+1); the next tiles travel from L2 straight into
+// LDS during a step's math.  LDS rows are padded by 16 bytes so that the rows
 // one operand read touches fall in distinct bank groups.  Workgroups are
 // numbered so that those of one (sequence, KV head) run on one XCD (one L2),
 // and for causal attention each head's latest (heaviest) query block starts
@@ -334,9 +334,6 @@ struct Lds2 {
   static constexpr int kRowV = kKT + kPadH;  // Vt tile row (one feature), halves
   static constexpr int kK = kKT * kRowK;
   static constexpr int kSlot = kK + D * kRowV;  // one slot: a K tile and a Vt tile
-  static constexpr int kChunks = kKT * D / 8;   // 16-byte chunks per tile (K or Vt)
-  static constexpr int kPer = kChunks / kThreads2;
-  static_assert(kChunks % kThreads2 == 0, "tile chunks must split evenly over the threads");
 };
 
 // S^T row rho of a 32-key half maps to key key32_of(rho) of that half: MFMA
