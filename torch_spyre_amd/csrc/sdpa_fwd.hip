@@ -327,6 +327,7 @@ constexpr int kQB = kWaves2 * kQW;  // queries per workgroup
 constexpr int kKT = 64;             // keys per step
 static_assert(kStick % kKT == 0, "the Vt padding must cover whole steps");
 constexpr int kPadH = 8;            // LDS row padding, halves (16 bytes)
+constexpr int kPrefetch = 3;        // LDS operand reads in flight ahead of the MFMA using them
 
 template <int D>
 struct Lds2 {
@@ -566,43 +567,83 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         psum = __builtin_amdgcn_fdot2(f16x2{pb[j][2 * e], pb[j][2 * e + 1]}, f16x2{1, 1}, psum, false);
     l_run += psum;
   };
-  // O^T += Vt[:, keys of half mt] P^T: k-steps 2mt, 2mt + 1.
-  auto pv_half = [&](const _Float16* vt, int mt, const f16x8 (&pb)[2]) {
-    const _Float16* vrow = vt + col * L::kRowV + 8 * half;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int dm = 0; dm < DM; ++dm) {
-        const f16x8 va = *reinterpret_cast<const f16x8*>(vrow + dm * 32 * L::kRowV + 16 * (2 * mt + j));
-        o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j], o[dm], 0, 0, 0);
-      }
+  // The 2 DK + 4 DM MFMAs of a step in issue order, each with its LDS operand
+  // fragment: 0 .. 2DK-1 the K operands of S(t+1) (half i / DK, k-step
+  // i % DK), then the Vt operands of O^T += Vt P^T, k-steps (half, j) =
+  // c / 2, c % 2 for c = (i - 2DK) / DM, O row tile dm = (i - 2DK) % DM.
+  // Each fragment is read kPrefetch MFMAs before its use: with reads issued
+  // only just ahead, every MFMA waited out an LDS read.
+  constexpr int kNF = 2 * DK + 4 * DM;
+  // LDS element offsets of the Vt rows of the step's four 16-key columns,
+  // hidden from the compiler: otherwise it pairs reads whose addresses are
+  // 32 bytes apart and issues the earlier one late, beside the later one.
+  uint32_t vcol[4];
+  auto frag = [&](const _Float16* k1, int i) -> f16x8 {
+    if (i < 2 * DK)
+      return *reinterpret_cast<const f16x8*>(k1 + ((i / DK) * 32 + key32_of(col)) * L::kRowK + 8 * half +
+                                             16 * (i % DK));
+    i -= 2 * DK;
+    return *reinterpret_cast<const f16x8*>(lds + vcol[i / DM] + (i % DM) * 32 * L::kRowV);
+  };
+  // Keeps a region's operand reads interleaved one per MFMA (n of each).
+  auto interleave_reads = [](int n) {
+    for (int i = 0; i < n; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
   };
 
   // Step t: LDS holds K(t+1) in slot (t+1)&1 and V(t) in slot t&1, cur
-  // holds S(t); the step loads K(t+2) and V(t+1) and leaves S(t+1) in nxt.  The MFMAs of S(t+1) and of step t's P V overlap step t's softmax:
-  // each scheduling region pairs one MFMA group with one VALU group (and
-  // bounds how far operand reads are hoisted).  At a wavefront's last active
-  // step S(t+1) reads a stale K slot and is never used.
+  // holds S(t); the step loads K(t+2) and V(t+1) and leaves S(t+1) in nxt.
+  // The MFMAs of S(t+1) and of step t's P V overlap step t's softmax: each
+  // scheduling region pairs one MFMA group with one VALU group.  At a
+  // wavefront's last active step S(t+1) reads a stale K slot and is never
+  // used.
   auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
     const _Float16* k1 = lds + ((t + 1) & 1) * L::kSlot;
-    const _Float16* vt = lds + (t & 1) * L::kSlot + L::kK;
     // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces V(t-1);
     // both land during this step's math.
     if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
     if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
     if (active(t)) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        vcol[c] = static_cast<uint32_t>((t & 1) * L::kSlot + L::kK + col * L::kRowV + 8 * half + 16 * c);
+        asm volatile("" : "+v"(vcol[c]));
+      }
+      f16x8 fr[kNF];
+#pragma unroll
+      for (int i = 0; i < kPrefetch; ++i) fr[i] = frag(k1, i);
+      // MFMA i, then the read of fragment i + kPrefetch.
+      auto mfma = [&](int i, const f16x8& b, f32x16& acc) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[i], b, acc, 0, 0, 0);
+        if (i + kPrefetch < kNF) fr[i + kPrefetch] = frag(k1, i + kPrefetch);
+      };
       if (edge(t)) mask_step(t, cur);
-      nxt[0] = qk(k1, 0);
+      nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < DK; ++ks) mfma(ks, qv[ks], nxt[0]);
+      interleave_reads(DK);
       update_max(cur, nxt[0]);
       const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
       f16x8 p0[2], p1[2];
-      nxt[1] = qk(k1, 1);
+      nxt[1] = PRESCALED ? neg_m_tile : f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < DK; ++ks) mfma(DK + ks, qv[ks], nxt[1]);
       softmax_half(cur[0], neg_m, p0);
+      interleave_reads(DK);
       __builtin_amdgcn_sched_barrier(0);
-      pv_half(vt, 0, p0);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
       softmax_half(cur[1], neg_m, p1);
+      interleave_reads(2 * DM);
       __builtin_amdgcn_sched_barrier(0);
-      pv_half(vt, 1, p1);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + 2 * DM + j * DM + dm, p1[j], o[dm]);
     }
     dma_wait();
     __syncthreads();
