@@ -156,7 +156,7 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     gg = torch.Generator(device=dev).manual_seed(seed + 1)
 
     # dense MHA decode: q [1, 8, 1, 64], k/v [1, 8, 512, 64], scale 1/8 (launch-bound:
-    # absolute µs; the call relays K/V into pages, then runs the paged kernel)
+    # absolute µs; the call restickifies V into the workspace, then runs the SDPA forward kernel)
     q1 = torch.randn((1, 8, 1, 64), generator=gg, device=dev).half()
     k1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
     v1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
