@@ -62,6 +62,15 @@ __device__ __forceinline__ float wave_xor(float x, int m) { return __shfl_xor(x,
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// fp32 -> fp16 of a value already rounded to fp32.  The empty asm keeps the
+// compiler from fusing the product before it into a mixed-precision FMA
+// (one rounding instead of two), which it does in some kernels and not in
+// others: the split and merge passes must round their outputs alike.
+__device__ __forceinline__ _Float16 to_f16(float x) {
+  asm volatile("" : "+v"(x));
+  return static_cast<_Float16>(x);
+}
+
 struct SplitArgs {
   const _Float16* q;
   const _Float16* k;
@@ -400,15 +409,14 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
     const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
     _Float16* op = a.out + row * D;
     const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
+    // Empty context: zeros, as torch's CPU SDPA returns.  One reciprocal:
+    // a division per element cost the single-round step ~2 %.
+    const float inv = ctx == 0 ? 0.f : (bad ? NAN : 1.f / l);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       f16x4 r;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        // Empty context: zeros, as torch's CPU SDPA returns.
-        const float x = ctx == 0 ? 0.f : (bad ? NAN : o[db][v] / l);
-        r[v] = static_cast<_Float16>(x);
-      }
+      for (int v = 0; v < 4; ++v) r[v] = to_f16(o[db][v] * inv);
       *reinterpret_cast<f16x4*>(op + 16 * db + 4 * grp) = r;
     }
     if (a.lse && grp == 0) a.lse[row] = ctx == 0 ? -INFINITY : (m + log2f(l)) * kLn2;
@@ -543,9 +551,9 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
     }
     M = mc;
   }
-  float res = acc / L;
+  float res = acc * (1.f / L);  // as the split kernel rounds it: one pass and two agree bit for bit
   if (ctx_raw > a.max_ctx) res = NAN;  // caller broke the max_context_len contract
-  o[d] = static_cast<_Float16>(res);
+  o[d] = to_f16(res);
   if (a.lse && d == 0) a.lse[static_cast<int64_t>(b) * a.Hq + h] = (M + log2f(L)) * kLn2;
 }
 
