@@ -27,8 +27,9 @@
 // form the dense N dimension, so K and V are read once for all g heads.
 // The token order of the QK rows is permuted so that each lane's P values
 // are exactly the 8 consecutive tokens the PV B operand needs.  The
-// wavefronts' partials (unnormalised O, running max, row sum) are combined
-// in registers through LDS, pairwise in log2(kWaves) rounds.  A sequence
+// wavefronts' partials (unnormalised O, running max, row sum) meet in LDS
+// behind one barrier, and every thread folds output elements over them in
+// wavefront order (a pairwise tree cost four more barriers).  A sequence
 // that fits one chunk (every sequence when max_context_len <= kWaves *
 // split_tokens) is then finished by its workgroup: fp16 out and LSE are
 // written directly and pass 2 is not launched.  Otherwise the chunk's
@@ -341,49 +342,11 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   l_out = l_run;
 }
 
-// Combines the kWaves wavefronts' partials of one workgroup, pairwise in
-// log2(kWaves) rounds through LDS: in each round the upper half of the
-// remaining wavefronts stores (o, m, l) lane by lane and the lower half folds
-// it into its registers with the online-softmax rescale.  Lanes of the two
-// wavefronts hold the same (head, d) elements, so the exchange is
-// lane-to-lane.  Wavefront 0 ends with the workgroup's partial.  Every
-// wavefront of the workgroup must call this (it has barriers).
-template <int D>
-__device__ __forceinline__ void combine_waves(f32x4 (&o)[D / 16], float& m, float& l, int wave,
-                                              int lane) {
-  constexpr int DB = D / 16;
-  __shared__ f32x4 s_o[kWaves / 2][DB][64];
-  __shared__ float s_m[kWaves / 2][64], s_l[kWaves / 2][64];
-#pragma unroll
-  for (int half = kWaves / 2; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
-      const int s = wave - half;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) s_o[s][db][lane] = o[db];
-      s_m[s][lane] = m;
-      s_l[s][lane] = l;
-    }
-    __syncthreads();
-    if (wave < half) {
-      const float m2 = s_m[wave][lane], l2 = s_l[wave][lane];
-      const float M = fmaxf(m, m2);
-      // Both empty: M = -inf, and exp2(-inf - -inf) would be NaN.
-      const float a1 = M == -INFINITY ? 0.f : fast_exp2(m - M);
-      const float a2 = M == -INFINITY ? 0.f : fast_exp2(m2 - M);
-      l = l * a1 + l2 * a2;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) o[db] = o[db] * a1 + s_o[wave][db][lane] * a2;
-      m = M;
-    }
-    if (half > 1) __syncthreads();  // the slots are stored again next round
-  }
-}
-
 // Work item (sequence b, chunk c, KV head kvh), run by all kWaves
-// wavefronts of the workgroup.  Wavefront 0 writes the result: fp16 out and
-// LSE when the sequence has one chunk and out is given, else the chunk's
-// partial (O^T rows as 16 contiguous bytes per lane and db; m, l) into the
-// workspace for the merge pass.
+// wavefronts of the workgroup.  The wavefronts' partials are combined in LDS
+// and the whole workgroup writes the result: fp16 out and LSE when the
+// sequence has one chunk and out is given, else the chunk's partial (O per
+// q head and feature; m, l) into the workspace for the merge pass.
 template <int D>
 __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int kvh, int wave,
                                          int lane) {
@@ -401,35 +364,59 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
   f32x4 o[DB];
   float m, l;
   stream_pages<D>(a, b, kvh, w0, w1 - w0, ctx, lane, o, m, l);
-  combine_waves<D>(o, m, l, wave, lane);
-  const int col = lane & 15, grp = lane >> 4;
-  if (wave != 0 || col >= a.g) return;
-  if (a.out && nch == 1) {
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-    const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
-    _Float16* op = a.out + row * D;
-    const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
-    // Empty context: zeros, as torch's CPU SDPA returns.  One reciprocal:
-    // a division per element cost the single-round step ~2 %.
-    const float inv = ctx == 0 ? 0.f : (bad ? NAN : 1.f / l);
+  // Every wavefront's partial goes to LDS once; then each thread folds
+  // output elements over the kWaves partials, in wavefront order.  Lane
+  // (col, grp) holds O^T[d = 16 db + 4 grp + v][col] in o[db][v]; a row of
+  // 16 columns is padded so that the fold's reads of columns < 4 (the usual
+  // group size) fall in distinct banks.
+  constexpr int kColPad = 4;
+  __shared__ f32x4 s_o[kWaves][DB][4][16 + kColPad];
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  {
+    const int col = lane & 15, grp = lane >> 4;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      f16x4 r;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) r[v] = to_f16(o[db][v] * inv);
-      *reinterpret_cast<f16x4*>(op + 16 * db + 4 * grp) = r;
+    for (int db = 0; db < DB; ++db) s_o[wave][db][grp][col] = o[db];
+    if (grp == 0) {
+      s_m[wave][col] = m;
+      s_l[wave][col] = l;
     }
-    if (a.lse && grp == 0) a.lse[row] = ctx == 0 ? -INFINITY : (m + log2f(l)) * kLn2;
-    return;
   }
+  __syncthreads();
+  const bool single = a.out && nch == 1;
+  const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
   const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks + c;
-  float* wo = a.ws + (slot * a.g + col) * D;
+  for (int e = static_cast<int>(threadIdx.x); e < a.g * D; e += kThreads) {
+    // e -> (db, grp, col, v), v fastest, then col < g, then grp.
+    const int v = e & 3;
+    const int r = e >> 2;
+    const int col = r % a.g, r2 = r / a.g;
+    const int grp = r2 & 3, db = r2 >> 2;
+    const int d = 16 * db + 4 * grp + v;
+    float M = -INFINITY;
 #pragma unroll
-  for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(wo + 16 * db + 4 * grp) = o[db];
-  if (grp == 0) {
-    float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D + (slot * a.g + col) * 2;
-    wm[0] = m;
-    wm[1] = l;
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][col]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      // Empty partials (m = -inf) weigh 0; all empty: M = -inf, L = O = 0.
+      const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
+      L += s_l[w][col] * sc;
+      O += s_o[w][db][grp][col][v] * sc;
+    }
+    if (single) {
+      const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
+      // Empty context: zeros, as torch's CPU SDPA returns.
+      const float inv = ctx == 0 ? 0.f : (bad ? NAN : 1.f / L);
+      a.out[row * D + d] = to_f16(O * inv);
+      if (a.lse && d == 0) a.lse[row] = ctx == 0 ? -INFINITY : (M + log2f(L)) * kLn2;
+    } else {
+      a.ws[(slot * a.g + col) * D + d] = O;
+      if (d == 0) {
+        float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D + (slot * a.g + col) * 2;
+        wm[0] = M;
+        wm[1] = L;
+      }
+    }
   }
 }
 
