@@ -41,9 +41,9 @@ METRIC = "decode-attn µs/step + achieved HBM GB/s (% peak); relayout GB/s"
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per decode_split_list_kernel launch at split 512, from rocprofv3
 # --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by the same
-# counters on torch's 32 MiB device copy (x1.99860 and x1.0): 537.07 MB read
+# counters on torch's 32 MiB device copy (x1.99857 and x1.0): 536.99 MB read
 # + 0.26 MB written (profiles/decode_attention_llama3_8b_b32_ctx4096_hbm_counters.md).
-TRAFFIC_BYTES = 537_335_256
+TRAFFIC_BYTES = 537_252_164
 B, HQ, HKV, D, CTX, PAGE, SPLIT = 32, 32, 8, 128, 4096, 64, 512
 
 
@@ -146,9 +146,9 @@ def cpu_relayout_baseline(x, budget_s=1.0):
 
 
 def more_configs(tsa, dev, stream, steps, warmup, seed):
-    """The ragged batch and the long-context append + attend step, timed the
-    same way (one cache each: both are far larger than the last-level
-    cache)."""
+    """The dense decode call, the ragged batch, the long-context append +
+    attend step and prefill SDPA, timed the same way (the two paged caches
+    are far larger than the last-level cache)."""
     import torch
 
     res = {}
