@@ -134,12 +134,17 @@ def test_config3_llama3_8b_full(cuda):
     assert_close(out, ref)
 
 
+@pytest.mark.parametrize("split", [256, 64])
 @pytest.mark.parametrize("g", [1, 2, 4, 8, 16])
-def test_gqa_groups(cuda, g):
+def test_gqa_groups(cuda, g, split):
+    """Every group size up to the MFMA's 16 columns.  Split 256: each
+    sequence is one chunk, finished by its workgroup (whose threads fold
+    g x D output elements, several each when g > 4); split 64: chunks of 512
+    tokens, so 700 and 1500 go through the chunk partials and the merge."""
     Hkv, D = 2, 128
     lens = [1, 64, 100, 700, 1500]
     cache, table, lens_t, q = make_case(cuda, len(lens), g * Hkv, Hkv, D, lens, SEED + g)
-    out = run(cache, table, lens_t, q, cuda, split_tokens=256)
+    out = run(cache, table, lens_t, q, cuda, split_tokens=split)
     ref = oracle_rows(cache, table, lens_t, q, list(range(len(lens))), 1 / math.sqrt(D))
     assert_close(out, ref)
 
