@@ -197,8 +197,10 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
 #define SPYRE_MASK_F32 2  /* additive fp32 bias                */
 #define SPYRE_MASK_BOOL 3 /* uint8/bool: nonzero = attend      */
 
-/* Workspace bytes needed by spyre_sdpa_fwd_f16: V re-laid out with its
- * sticks along tokens, B * Hkv * D * ceil(Skv / 64) * 64 fp16. */
+/* Workspace bytes needed by spyre_sdpa_fwd_f16 with an attention mask: V
+ * re-laid out with its sticks along tokens, B * Hkv * D * ceil(Skv / 64) * 64
+ * fp16.  Calls without a mask (plain or causal) need no workspace: they read
+ * V as it lies. */
 size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
 
 /* Scaled dot-product attention forward (prefill, any Sq):

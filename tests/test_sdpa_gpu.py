@@ -192,6 +192,27 @@ def test_overrideable_tuple_and_custom_op(cuda):
     assert torch.equal(out, res[0]) and torch.equal(lse, res[1])
 
 
+def test_workspace_only_for_masks(cuda):
+    """Calls without a mask read V as it lies (no workspace, none allocated):
+    with and without a caller's workspace the bits agree; K and V with
+    different row strides; a masked call still checks its workspace."""
+    import torch_spyre_amd as tsa
+
+    q = randn((1, 8, 300, 128), SEED + 40).to(cuda)
+    k = randn((1, 2, 333, 128), SEED + 41).to(cuda)
+    v = randn((1, 333, 2, 128), SEED + 42).to(cuda).transpose(1, 2)  # row stride 256, K's is 128
+    for causal in (False, True):
+        a = tsa.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True)
+        ws = torch.empty(tsa.sdpa.workspace_bytes(1, 2, 333, 128), dtype=torch.uint8, device=cuda)
+        b = tsa.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True, workspace=ws)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        assert_close(a, OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), is_causal=causal))
+    mask = torch.zeros((300, 333), dtype=torch.float16, device=cuda)
+    with pytest.raises(ValueError):
+        tsa.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True,
+                                         workspace=torch.empty(16, dtype=torch.uint8, device=cuda))
+
+
 def test_argument_errors(cuda):
     import torch_spyre_amd as tsa
 

@@ -60,6 +60,12 @@ constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit format
 // 16 bytes per lane from buffer offset voff into LDS: lane l writes the 16
 // bytes at dst + 16 l (dst wave-uniform).  Lanes whose offset lies past the
 // buffer's range write zeros.
+// ds_read_b64_tr_b16 at LDS element p (see the V operand reads below).
+__device__ __forceinline__ short __attribute__((ext_vector_type(4))) tr_read4(const _Float16* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
+}
+
 __device__ __forceinline__ void load_lds16(Rsrc r, _Float16* dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
 }
@@ -303,22 +309,26 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(FwdArgs a) {
 //
 // One workgroup of kWaves2 wavefronts per 256 queries of one (sequence, q
 // head); wavefront w takes 32 of them.  Per 64-key step t the workgroup
-// stages the K tile [64 keys][D] and the Vt tile [D][64 keys] in LDS, and
-// every wavefront reads its MFMA operands from there:
+// stages the K tile and the V tile, both [64 keys][D] as K and V lie in
+// memory, in LDS, and every wavefront reads its MFMA operands from there:
 //   S^T[key, q] = K Q^T   2 x D/16 MFMA 32x32x16 (M = 32 keys, N = 32 queries)
-//   O^T[d, q] += Vt P^T   D/32 x 4 MFMA 32x32x16
+//   O^T[d, q] += V^T P^T  D/32 x 4 MFMA 32x32x16
+// The V^T operand (8 consecutive keys of one feature per lane) comes from
+// the row-major V tile through the transposing LDS read ds_read_b64_tr_b16,
+// so V needs no relayout before the kernel.
 // The loop is software-pipelined: K runs one step ahead of V, so while the
 // VALU computes step t's softmax the matrix cores already compute step
 // t+1's scores and then step t's P V.  Two LDS slots each hold K(t+1) /
 // K(t+2) and V(t) / V(t+1); the next tiles travel from L2 straight into
-// LDS during a step's math.  LDS rows are padded by 16 bytes so that the rows
-// one operand read touches fall in distinct bank groups.  Workgroups are
+// LDS during a step's math.  LDS rows are padded so that the rows one
+// operand read touches fall in distinct bank groups.  Workgroups are
 // numbered so that those of one (sequence, KV head) run on one XCD (one L2),
 // and for causal attention each head's latest (heaviest) query block starts
 // first.
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves2 = 8;
 constexpr int kThreads2 = kWaves2 * 64;
@@ -327,14 +337,16 @@ constexpr int kQB = kWaves2 * kQW;  // queries per workgroup
 constexpr int kKT = 64;             // keys per step
 static_assert(kStick % kKT == 0, "the Vt padding must cover whole steps");
 constexpr int kPadH = 8;            // LDS row padding, halves (16 bytes)
-constexpr int kPrefetch = 3;        // LDS operand reads in flight ahead of the MFMA using them
+constexpr int kPrefetch = 4;        // LDS operand reads in flight ahead of the MFMA using them
 
 template <int D>
 struct Lds2 {
   static constexpr int kRowK = D + kPadH;    // K tile row (one key), halves
-  static constexpr int kRowV = kKT + kPadH;  // Vt tile row (one feature), halves
+  // V tile row: padded so that a row step moves the transposed reads by 8
+  // (mod 64) banks (D = 128: 144 halves, D = 64: 72).
+  static constexpr int kRowV = D == 128 ? D + 16 : D + kPadH;
   static constexpr int kK = kKT * kRowK;
-  static constexpr int kSlot = kK + D * kRowV;  // one slot: a K tile and a Vt tile
+  static constexpr int kSlot = kK + kKT * kRowV;  // one slot: a K tile and a V tile
 };
 
 // S^T row rho of a 32-key half maps to key key32_of(rho) of that half: MFMA
@@ -363,13 +375,13 @@ __device__ __forceinline__ float sum_xor32(float x) {
 struct Fwd2Args {
   const _Float16* q;
   const _Float16* k;
-  const _Float16* vt;
+  const _Float16* v;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
-  int64_t vt_sb, vt_sh;
+  int64_t v_sb, v_sh, v_ss;
   _Float16* out;
   float* lse;
-  int B, Hq, Hkv, g, Sq, Skv, s64, causal, qblocks;
+  int B, Hq, Hkv, g, Sq, Skv, causal, qblocks;
   uint32_t n_items;
   int xcd_remap;
   float scale_log2;
@@ -426,20 +438,20 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     for (int ks = 0; ks < DK; ++ks) asm volatile("" : : "v"(qv[ks]));
   }
   const _Float16* kbase = a.k + b * a.k_sb + kvh * a.k_sh;
-  const _Float16* vbase = a.vt + b * a.vt_sb + kvh * a.vt_sh;
+  const _Float16* vbase = a.v + b * a.v_sb + kvh * a.v_sh;
 
   // Tiles move from L2 straight into LDS (buffer loads with the LDS flag):
   // lane l of a load writes the 16 bytes at M0 + 16 l, so load i of a tile
   // fills its 16-byte units 64 i .. 64 i + 63, padded rows included.  Lane
-  // l of load i fetches the unit's source; pad units and K rows past Skv get
-  // an offset past the buffer's range and are written as zeros.  Per-lane
+  // l of load i fetches the unit's source; pad units and K / V rows past Skv
+  // get an offset past the buffer's range and are written as zeros.  Per-lane
   // offsets are fixed for the whole loop; the step only moves the base.
   constexpr int kUK = L::kRowK / 8, kUV = L::kRowV / 8;  // 16-byte units per padded row
-  constexpr int kNK = kKT * kUK / 64, kNV = D * kUV / 64;  // loads per tile
-  static_assert(kKT * kUK % 64 == 0 && D * kUV % 64 == 0, "tiles must be whole loads");
+  constexpr int kNK = kKT * kUK / 64, kNV = kKT * kUV / 64;  // loads per tile
+  static_assert(kKT * kUK % 64 == 0 && kKT * kUV % 64 == 0, "tiles must be whole loads");
   constexpr int kJK = (kNK + kWaves2 - 1) / kWaves2, kJV = (kNV + kWaves2 - 1) / kWaves2;
   constexpr uint32_t kOob = 0x80000000u;  // past kBufRange
-  uint32_t k_off[kJK], k_row[kJK], v_off[kJV];
+  uint32_t k_off[kJK], k_row[kJK], v_off[kJV], v_row[kJV];
 #pragma unroll
   for (int j = 0; j < kJK; ++j) {
     const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUK, ch = u % kUK;
@@ -450,7 +462,9 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 #pragma unroll
   for (int j = 0; j < kJV; ++j) {
     const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUV, ch = u % kUV;
-    v_off[j] = ch == kUV - 1 ? kOob : static_cast<uint32_t>(row * a.s64 + 8 * ch) * 2;
+    const bool pad = ch >= D / 8;
+    v_row[j] = pad ? kOob : static_cast<uint32_t>(row);
+    v_off[j] = pad ? kOob : (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_ss) + 8 * ch) * 2;
   }
   // K rows kb .. kb + 63 into slot `slot` (rows >= Skv as zeros).
   auto dma_k = [&](int kb, int slot) {
@@ -461,13 +475,15 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       if (wave + kWaves2 * j < kNK)
         load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_row[j] < rows_left ? k_off[j] : kOob);
   };
-  // Vt columns kb .. kb + 63 (zero-padded up to s64 in the workspace).
+  // V rows kb .. kb + 63 into slot `slot` (rows >= Skv as zeros, so that a
+  // masked key's P = 0 never meets stale bits).
   auto dma_v = [&](int kb, int slot) {
-    const Rsrc r = make_rsrc(vbase + kb, kBufRange);
+    const Rsrc r = make_rsrc(vbase + static_cast<int64_t>(kb) * a.v_ss, kBufRange);
+    const uint32_t rows_left = static_cast<uint32_t>(a.Skv - kb);
 #pragma unroll
     for (int j = 0; j < kJV; ++j)
       if (wave + kWaves2 * j < kNV)
-        load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_off[j]);
+        load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_row[j] < rows_left ? v_off[j] : kOob);
   };
   // The loads must have landed before the barrier that publishes them.
   auto dma_wait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
@@ -569,27 +585,43 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   };
   // The 2 DK + 4 DM MFMAs of a step in issue order, each with its LDS operand
   // fragment: 0 .. 2DK-1 the K operands of S(t+1) (half i / DK, k-step
-  // i % DK), then the Vt operands of O^T += Vt P^T, k-steps (half, j) =
-  // c / 2, c % 2 for c = (i - 2DK) / DM, O row tile dm = (i - 2DK) % DM.
+  // i % DK), then the V^T operands of O^T += V^T P^T (two transposed reads
+  // each), k-steps (half, j) = c / 2, c % 2 for c = (i - 2DK) / DM, O row tile
+  // dm = (i - 2DK) % DM.
   // Each fragment is read kPrefetch MFMAs before its use: with reads issued
   // only just ahead, every MFMA waited out an LDS read.
   constexpr int kNF = 2 * DK + 4 * DM;
   // LDS element offsets of the Vt rows of the step's four 16-key columns,
   // hidden from the compiler: otherwise it pairs reads whose addresses are
   // 32 bytes apart and issues the earlier one late, beside the later one.
-  uint32_t vcol[4];
+  uint32_t vtr;  // this lane's V tile element for the transposed reads, in the step's slot
+  // Within each 16 lanes, lane s reads V[key 8 half + s / 4][d 16 (lane / 16 % 2) + 4 (s % 4)
+  // .. + 3]; ds_read_b64_tr_b16 hands lane j of the 16 the four keys of column d + j.
+  const uint32_t vtr_lane = static_cast<uint32_t>((8 * half + ((lane & 15) >> 2)) * L::kRowV +
+                                                  16 * ((lane >> 4) & 1) + 4 * (lane & 3));
+  auto tr4 = [&](uint32_t e) { return tr_read4(lds + e); };
   auto frag = [&](const _Float16* k1, int i) -> f16x8 {
     if (i < 2 * DK)
       return *reinterpret_cast<const f16x8*>(k1 + ((i / DK) * 32 + key32_of(col)) * L::kRowK + 8 * half +
                                              16 * (i % DK));
     i -= 2 * DK;
-    return *reinterpret_cast<const f16x8*>(lds + vcol[i / DM] + (i % DM) * 32 * L::kRowV);
+    // keys 16 (i / DM) + 8 half .. + 7 of feature 32 (i % DM) + col
+    const uint32_t e = vtr + (16 * (i / DM)) * L::kRowV + 32 * (i % DM);
+    const v4i16 lo = tr4(e), hi = tr4(e + 4 * L::kRowV);
+    return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
   // Keeps a region's operand reads interleaved one per MFMA (n of each).
-  auto interleave_reads = [](int n) {
-    for (int i = 0; i < n; ++i) {
+  // Keeps a region's operand reads interleaved with its MFMAs i0 .. i1 - 1:
+  // each MFMA, then the reads of the fragment kPrefetch ahead (two for a V
+  // fragment).
+  auto interleave_reads = [](int i0, int i1) {
+    for (int i = i0; i < i1; ++i) {
+      const int f = i + kPrefetch;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      if (f < 2 * DK)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read (K)
+      else if (f < kNF)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two (V, transposed)
     }
   };
 
@@ -606,11 +638,8 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
     if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
     if (active(t)) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        vcol[c] = static_cast<uint32_t>((t & 1) * L::kSlot + L::kK + col * L::kRowV + 8 * half + 16 * c);
-        asm volatile("" : "+v"(vcol[c]));
-      }
+      vtr = static_cast<uint32_t>((t & 1) * L::kSlot + L::kK) + vtr_lane;
+      asm volatile("" : "+v"(vtr));
       f16x8 fr[kNF];
 #pragma unroll
       for (int i = 0; i < kPrefetch; ++i) fr[i] = frag(k1, i);
@@ -623,7 +652,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
       for (int ks = 0; ks < DK; ++ks) mfma(ks, qv[ks], nxt[0]);
-      interleave_reads(DK);
+      interleave_reads(0, DK);
       update_max(cur, nxt[0]);
       const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
       f16x8 p0[2], p1[2];
@@ -631,14 +660,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 #pragma unroll
       for (int ks = 0; ks < DK; ++ks) mfma(DK + ks, qv[ks], nxt[1]);
       softmax_half(cur[0], neg_m, p0);
-      interleave_reads(DK);
+      interleave_reads(DK, 2 * DK);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
       softmax_half(cur[1], neg_m, p1);
-      interleave_reads(2 * DM);
+      interleave_reads(2 * DK, 2 * DK + 2 * DM);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -733,13 +762,15 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     SPYRE_REQUIRE(static_cast<int64_t>(Skv) * mask_strides[3] < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
                   "mask row spans 2^31 elements or more");
   }
-  const size_t need = spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D);
+  // Only the masked kernel reads V through the workspace (V with its sticks
+  // along tokens); calls without a mask need none.
+  const size_t need = mask_kind != kNoMask ? spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D) : 0;
   SPYRE_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
                 SPYRE_ENOSPC, "workspace %zu < %zu bytes (or misaligned)", workspace_bytes, need);
   if (Sq == 0) return SPYRE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int s64 = static_cast<int>(s64_of(Skv));
-  if (Skv > 0) {
+  if (Skv > 0 && mask_kind != kNoMask) {
     VtArgs va{static_cast<const _Float16*>(v), v_strides[0], v_strides[1], v_strides[2],
               static_cast<_Float16*>(workspace), Hkv, Skv, s64, D,
               static_cast<int64_t>(B) * Hkv * (s64 / 64) * (D / 64)};
@@ -761,10 +792,11 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
   fa.k_ss = k_strides[2];
   fa.vt_sb = static_cast<int64_t>(Hkv) * D * s64;
   fa.vt_sh = static_cast<int64_t>(D) * s64;
-  // Buffer extents (bytes) of one head: K rows 0..Skv-1, Vt [D, s64].
+  // Buffer extents (bytes) of one head: K and V rows 0..Skv-1, Vt [D, s64].
   const int64_t k_span = Skv > 0 ? ((static_cast<int64_t>(Skv) - 1) * k_strides[2] + D) * 2 : 0;
+  const int64_t v_span = Skv > 0 ? ((static_cast<int64_t>(Skv) - 1) * v_strides[2] + D) * 2 : 0;
   const int64_t vt_span = static_cast<int64_t>(D) * s64 * 2;
-  SPYRE_REQUIRE(k_span <= kBufRange && vt_span <= kBufRange, SPYRE_EUNSUPPORTED,
+  SPYRE_REQUIRE(k_span <= kBufRange && v_span <= kBufRange && vt_span <= kBufRange, SPYRE_EUNSUPPORTED,
                 "one head of K or V spans 2 GiB or more");
   fa.k_bytes = static_cast<uint32_t>(k_span);
   fa.vt_bytes = static_cast<uint32_t>(vt_span);
@@ -792,15 +824,16 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     Fwd2Args f2{};
     f2.q = fa.q;
     f2.k = fa.k;
-    f2.vt = fa.vt;
+    f2.v = static_cast<const _Float16*>(v);
     f2.q_sb = fa.q_sb;
     f2.q_sh = fa.q_sh;
     f2.q_ss = fa.q_ss;
     f2.k_sb = fa.k_sb;
     f2.k_sh = fa.k_sh;
     f2.k_ss = fa.k_ss;
-    f2.vt_sb = fa.vt_sb;
-    f2.vt_sh = fa.vt_sh;
+    f2.v_sb = v_strides[0];
+    f2.v_sh = v_strides[1];
+    f2.v_ss = v_strides[2];
     f2.out = fa.out;
     f2.lse = fa.lse;
     f2.B = B;
@@ -809,7 +842,6 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.g = fa.g;
     f2.Sq = Sq;
     f2.Skv = Skv;
-    f2.s64 = s64;
     f2.causal = fa.causal;
     f2.qblocks = (Sq + kQB - 1) / kQB;
     const int64_t items = static_cast<int64_t>(B) * Hq * f2.qblocks;

@@ -92,17 +92,20 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
     s = 1.0 / math.sqrt(D) if scale is None else float(scale)
     out = torch.empty((B, Sq, Hq, D), dtype=torch.float16, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
-    need = workspace_bytes(B, Hkv, Skv, D)
-    if workspace is None:
-        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
-    elif workspace.numel() * workspace.element_size() < need:
+    # Only masked calls read V through the workspace.
+    need = workspace_bytes(B, Hkv, Skv, D) if kind != MASK_NONE else 0
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    elif workspace is not None and workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, need {need}")
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     rc = _lib.lib().spyre_sdpa_fwd_f16(
         q.data_ptr(), _lib.i64_array(q.stride()[:3]), k.data_ptr(), _lib.i64_array(k.stride()[:3]),
         v.data_ptr(), _lib.i64_array(v.stride()[:3]), mask.data_ptr() if mask is not None else None,
         kind, mstrides, int(bool(is_causal)), s, out.data_ptr(),
-        lse.data_ptr() if lse is not None else None, workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), B, Hq, Hkv, Sq, Skv, D, _stream_ptr(q.device))
+        lse.data_ptr() if lse is not None else None, ws_ptr, ws_bytes, B, Hq, Hkv, Sq, Skv, D,
+        _stream_ptr(q.device))
     _lib.check("spyre_sdpa_fwd_f16", rc)
     out = out.transpose(1, 2)
     return (out, lse) if return_lse else out
