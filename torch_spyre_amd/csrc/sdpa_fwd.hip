@@ -342,9 +342,11 @@ constexpr int kPrefetch = 4;        // LDS operand reads in flight ahead of the 
 template <int D>
 struct Lds2 {
   static constexpr int kRowK = D + kPadH;    // K tile row (one key), halves
-  // V tile row: padded so that a row step moves the transposed reads by 8
-  // (mod 64) banks (D = 128: 144 halves, D = 64: 72).
-  static constexpr int kRowV = D == 128 ? D + 16 : D + kPadH;
+  // V tile row: a transposed read serves 32 lanes at once, 4 rows x 4
+  // 8-byte units in each of two column groups 32 bytes apart; a row step of
+  // 16 (D = 128: 160 halves) or 48 (D = 64: 96 halves) banks mod 64 puts all
+  // of them in distinct banks.
+  static constexpr int kRowV = D + 32;
   static constexpr int kK = kKT * kRowK;
   static constexpr int kSlot = kK + kKT * kRowV;  // one slot: a K tile and a V tile
 };
@@ -462,7 +464,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 #pragma unroll
   for (int j = 0; j < kJV; ++j) {
     const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUV, ch = u % kUV;
-    const bool pad = ch >= D / 8;
+    const bool pad = ch >= D / 8;  // kRowV / 8 - D / 8 pad units per row
     v_row[j] = pad ? kOob : static_cast<uint32_t>(row);
     v_off[j] = pad ? kOob : (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_ss) + 8 * ch) * 2;
   }
