@@ -15,7 +15,8 @@ Also timed: under "more_configs", the dense MHA decode call (q [1, 8, 1, 64], k/
 [1, 8, 512, 64]; absolute µs, launch-bound), the ragged batch (64 sequences, context
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
 heads, append one token at position 131072, attend over 131073 tokens) and
-prefill SDPA, causal and full (batch 1, 32 q / 8 KV heads, 4096 tokens);
+prefill SDPA, causal, full and with an fp16 / boolean [4096, 4096] mask
+(batch 1, 32 q / 8 KV heads, 4096 tokens);
 under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
 transpose-restick, rotating 9 buffer pairs (576 MiB), with torch's CPU
 view/permute/contiguous of the same closed forms as its CPU baseline.
@@ -224,6 +225,19 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
                    max(steps // 5, 3), 2, stream)
         flops = 4 * HQ * D * (S * (S + 1) / 2 if causal else S * S)
         res["prefill_b1_h32_8_s4096" + ("_causal" if causal else "")] = {
+            "us_per_step": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / PEAK_F16, 4), "flops": flops,
+            "kernels_per_step": 1}
+    # the same with a [4096, 4096] mask broadcast over heads: an fp16 bias
+    # ~ N(0, 1) and a boolean keep-mask (70 % kept); every pair is computed
+    ws = torch.empty(tsa.sdpa.workspace_bytes(1, HKV, S, D), dtype=torch.uint8, device=dev)
+    masks = {"mask_f16": torch.randn((S, S), generator=gg, device=dev).half(),
+             "mask_bool": torch.rand((S, S), generator=gg, device=dev) < 0.7}
+    for name, m in masks.items():
+        ms = timed(lambda i: tsa.scaled_dot_product_attention(q, k, v, attn_mask=m, enable_gqa=True, workspace=ws),
+                   max(steps // 5, 3), 2, stream)
+        flops = 4 * HQ * D * S * S
+        res["prefill_b1_h32_8_s4096_" + name] = {
             "us_per_step": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
             "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / PEAK_F16, 4), "flops": flops,
             "kernels_per_step": 1}

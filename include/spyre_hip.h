@@ -200,7 +200,10 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
 /* Workspace bytes needed by spyre_sdpa_fwd_f16 with an attention mask: V
  * re-laid out with its sticks along tokens, B * Hkv * D * ceil(Skv / 64) * 64
  * fp16.  Calls without a mask (plain or causal) need no workspace: they read
- * V as it lies. */
+ * V as it lies.  So do, in fact, fp16 and bool masks with key stride 1, a
+ * 16-byte aligned pointer and b / h / i strides of whole 16 bytes (staged in
+ * LDS beside K and V); masked calls pass the workspace all the same, since
+ * any other mask (fp32, unaligned) runs a kernel that reads V through it. */
 size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
 
 /* Scaled dot-product attention forward (prefill, any Sq):

@@ -123,6 +123,62 @@ def test_masks_broadcast(cuda, kind, shape):
     assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask))
 
 
+def _mask(kind, dims, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "bool":
+        m = torch.rand(dims, generator=g) > 0.3
+        m[..., 0] = True  # no fully masked row here
+        return m
+    return (torch.randn(dims, generator=g) * 2).to(torch.float16)
+
+
+@pytest.mark.parametrize("kind", ["f16", "bool"])
+@pytest.mark.parametrize("shape", ["qk", "b1qk", "1h1k", "bhqk"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_masks_staged_in_lds(cuda, kind, shape, D):
+    """fp16 and boolean masks whose rows are whole 16-byte units (Skv a
+    multiple of 16) are staged block by block beside K and V: ragged Sq,
+    a last step of 32 keys, GQA, every broadcast form."""
+    B, Hq, Hkv, Sq, Skv = 2, 8, 2, 100, 160
+    q = randn((B, Hq, Sq, D), SEED + 11)
+    k, v = randn((B, Hkv, Skv, D), SEED + 12), randn((B, Hkv, Skv, D), SEED + 13)
+    dims = {"qk": (Sq, Skv), "b1qk": (B, 1, Sq, Skv), "1h1k": (1, Hq, 1, Skv), "bhqk": (B, Hq, Sq, Skv)}[shape]
+    mask = _mask(kind, dims, SEED + 14)
+    out = run(cuda, q, k, v, attn_mask=mask, enable_gqa=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask))
+
+
+@pytest.mark.parametrize("kind", ["f16", "bool"])
+def test_staged_mask_ignores_bytes_past_skv(cuda, kind):
+    """A mask that is a view of wider rows: the bytes past Skv in each row
+    (NaN for fp16, keep for bool) belong to no key and change nothing; a
+    large scale (|scale log2 e| > 1) takes the unscaled-score form."""
+    Sq, Skv, D = 70, 96, 128
+    q, k, v = randn((1, 4, Sq, D), SEED + 15), randn((1, 4, Skv, D), SEED + 16), randn((1, 4, Skv, D), SEED + 17)
+    wide = _mask(kind, (Sq, Skv + 32), SEED + 18)
+    wide[:, Skv:] = True if kind == "bool" else float("nan")
+    mask = wide.to(cuda)[:, :Skv]  # sliced on the device, so its rows keep their stride
+    assert mask.stride() == (Skv + 32, 1)
+    for scale in (None, 2.0):
+        out = run(cuda, q, k, v, attn_mask=mask, scale=scale)
+        assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask.cpu().contiguous(), scale=scale))
+
+
+@pytest.mark.parametrize("kind", ["f16", "bool"])
+def test_staged_mask_fully_masked_rows(cuda, kind):
+    """Rows with every key masked (a whole wavefront's block, and single
+    rows) give zeros and a -inf logsumexp through the staged path too."""
+    Sq, Skv = 80, 128
+    q, k, v = randn((1, 2, Sq, 64), SEED + 19), randn((1, 2, Skv, 64), SEED + 20), randn((1, 2, Skv, 64), SEED + 21)
+    mask = _mask(kind, (Sq, Skv), SEED + 22)
+    dead = [3, *range(32, 64), 79]  # rows 32 .. 63: one wavefront's whole block
+    mask[dead] = False if kind == "bool" else -float("inf")
+    out, lse = run(cuda, q, k, v, attn_mask=mask, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask))
+    assert not out[:, :, dead].float().abs().sum()
+    assert torch.isinf(lse[:, :, dead]).all() and (lse[:, :, dead] < 0).all()
+
+
 def test_fully_masked_rows_give_zeros_and_minus_inf_lse(cuda):
     q, k, v = randn((1, 2, 40, 64), SEED + 5), randn((1, 2, 33, 64), SEED + 6), randn((1, 2, 33, 64), SEED + 7)
     mask = torch.zeros((40, 33))

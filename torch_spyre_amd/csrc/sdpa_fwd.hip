@@ -378,6 +378,9 @@ struct Fwd2Args {
   const _Float16* q;
   const _Float16* k;
   const _Float16* v;
+  const void* mask;          // fp16 bias or uint8 keep-mask, keys contiguous
+  int64_t m_sb, m_sh, m_sq;  // elements
+  uint32_t m_bytes;          // extent of one (sequence, q head) of the mask
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -389,17 +392,33 @@ struct Fwd2Args {
   float scale_log2;
 };
 
+// A wavefront's mask block for one step: its 32 queries x the step's 64 keys,
+// rows padded by 16 bytes, staged in LDS by buffer loads like the K / V
+// tiles (whole 1 KB loads; units past the block arrive as zeros in a spare
+// tail).
+template <int MK> struct MaskTile {
+  static constexpr int kRowU = 0, kDataU = 0, kLoads = 0, kBytes = 0, kEsz = 1;
+};
+template <> struct MaskTile<kMaskF16> {  // 128 + 16 bytes per row
+  static constexpr int kRowU = 9, kDataU = 8, kLoads = 5, kBytes = kLoads * 1024, kEsz = 2;
+};
+template <> struct MaskTile<kMaskBool> {  // 64 + 16 bytes per row
+  static constexpr int kRowU = 5, kDataU = 4, kLoads = 3, kBytes = kLoads * 1024, kEsz = 1;
+};
+
 // PRESCALED (|scale log2 e| <= 1, so q * that never overflows fp16): Q is
 // multiplied by scale log2 e once, and every step's scores leave the MFMA
 // already as exponents: the first QK MFMA starts from a tile holding -m
 // (the running max), so P = exp2(S) needs no per-score FMA.  Otherwise the
 // scale's sign is folded into Q and its magnitude into the exponent's FMA.
-template <int D, bool PRESCALED>
+template <int D, bool PRESCALED, int MK>
 __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   using L = Lds2<D>;
+  using MT = MaskTile<MK>;
   constexpr int DK = D / 16;  // QK k-steps
   constexpr int DM = D / 32;  // O row tiles
-  __shared__ __align__(16) _Float16 lds[2 * L::kSlot];
+  // Two K / V slots, then (masked calls) two mask blocks per wavefront.
+  __shared__ __align__(16) _Float16 lds[2 * L::kSlot + kWaves2 * MT::kBytes];
 
   // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * g + gi: the
   // blocks of one (sequence, KV head) are consecutive, latest query block
@@ -487,6 +506,33 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       if (wave + kWaves2 * j < kNV)
         load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_row[j] < rows_left ? v_off[j] : kOob);
   };
+  // The wavefront's mask block of keys kb .. kb + 63 into its slot `slot`:
+  // rows past Sq and bytes past the (sequence, head) slice arrive as zeros.
+  // Offsets are from the wavefront's first query row; the descriptor's range
+  // ends with the (sequence, head) slice.
+  uint32_t m_off[MT::kLoads > 0 ? MT::kLoads : 1];
+  const char* mbase = nullptr;
+  uint32_t m_left = 0;  // bytes of the slice from row q0, key 0
+  if constexpr (MK != kNoMask) {
+    const int64_t row0 = static_cast<int64_t>(min(q0, a.Sq - 1)) * a.m_sq * MT::kEsz;
+    mbase = static_cast<const char*>(a.mask) + (b * a.m_sb + h * a.m_sh) * MT::kEsz + row0;
+    m_left = a.m_bytes - static_cast<uint32_t>(row0);
+#pragma unroll
+    for (int j = 0; j < MT::kLoads; ++j) {
+      const int u = 64 * j + lane, row = u / MT::kRowU, ch = u % MT::kRowU;
+      const bool ok = row < kQW && ch < MT::kDataU && q0 + row < a.Sq;
+      m_off[j] = ok ? static_cast<uint32_t>((row * a.m_sq) * MT::kEsz + 16 * ch) : kOob;
+    }
+  }
+  auto mask_block = [&](int slot) { return lds + 2 * L::kSlot + (slot * kWaves2 + wave) * (MT::kBytes / 2); };
+  auto dma_m = [&](int kb, int slot) {
+    if constexpr (MK != kNoMask) {
+      const uint32_t done = static_cast<uint32_t>(kb) * MT::kEsz;  // < Skv esz <= m_left
+      const Rsrc r = make_rsrc(reinterpret_cast<const _Float16*>(mbase + done), m_left - done);
+#pragma unroll
+      for (int j = 0; j < MT::kLoads; ++j) load_lds16(r, mask_block(slot) + 512 * j, m_off[j]);
+    }
+  };
   // The loads must have landed before the barrier that publishes them.
   auto dma_wait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
@@ -533,6 +579,33 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         const int kr = mt * 32 + key32_of(8 * (rr >> 2) + (rr & 3));  // key - t kKT - 8 half
         s[mt][rr] = kr <= kl ? s[mt][rr] : -INFINITY;
       }
+  };
+  // The step's mask from the wavefront's block in LDS: registers 4i + v of
+  // half mt are keys 32 mt + 16 (i / 2) + 8 half + 4 (i % 2) + v of query
+  // col, four consecutive keys per read.  A bias is added in the scores'
+  // units (PRESCALED: log2 units, else divided by |scale|), a keep-mask
+  // sends dropped scores to -inf.
+  const float bias_mul = PRESCALED ? kLog2e : kLog2e / scale_abs;
+  auto apply_mask = [&](int t, f32x16 (&s)[2]) {
+    if constexpr (MK != kNoMask) {
+      const char* row = reinterpret_cast<const char*>(mask_block(t & 1)) + col * (16 * MT::kRowU);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int k4 = 32 * mt + 16 * (i >> 1) + 8 * half + 4 * (i & 1);
+          if constexpr (MK == kMaskF16) {
+            const f16x4 m4 = *reinterpret_cast<const f16x4*>(row + 2 * k4);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) s[mt][4 * i + v] = __builtin_fmaf(static_cast<float>(m4[v]), bias_mul, s[mt][4 * i + v]);
+          } else {
+            const uint32_t m4 = *reinterpret_cast<const uint32_t*>(row + k4);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              s[mt][4 * i + v] = ((m4 >> (8 * v)) & 0xffu) != 0 ? s[mt][4 * i + v] : -INFINITY;
+          }
+        }
+    }
   };
   // The running max (log2 domain) moves only when a score of the step
   // exceeds it by more than 2^8, so P <= 256 (fine in fp16) and most steps
@@ -639,6 +712,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     // both land during this step's math.
     if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
     if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
+    if (t + 1 < n_tiles) dma_m((t + 1) * kKT, (t + 1) & 1);
     if (active(t)) {
       vtr = static_cast<uint32_t>((t & 1) * L::kSlot + L::kK) + vtr_lane;
       asm volatile("" : "+v"(vtr));
@@ -650,6 +724,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[i], b, acc, 0, 0, 0);
         if (i + kPrefetch < kNF) fr[i + kPrefetch] = frag(k1, i + kPrefetch);
       };
+      apply_mask(t, cur);
       if (edge(t)) mask_step(t, cur);
       nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
@@ -687,6 +762,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   if (n_tiles > 0) {
     dma_k(0, 0);
     dma_v(0, 0);
+    dma_m(0, 0);
   }
   if (n_tiles > 1) dma_k(kKT, 1);
   dma_wait();
@@ -718,6 +794,19 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     }
   if (a.lse && half == 0)
     a.lse[(static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi] = l > 0.f ? (m_run + log2f(l)) * kLn2 : -INFINITY;
+}
+
+template <int MK>
+void launch_lds(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
+  const dim3 grid(f2.n_items);
+  if (D == 128 && prescaled)
+    sdpa_fwd_lds_kernel<128, true, MK><<<grid, kThreads2, 0, st>>>(f2);
+  else if (D == 128)
+    sdpa_fwd_lds_kernel<128, false, MK><<<grid, kThreads2, 0, st>>>(f2);
+  else if (prescaled)
+    sdpa_fwd_lds_kernel<64, true, MK><<<grid, kThreads2, 0, st>>>(f2);
+  else
+    sdpa_fwd_lds_kernel<64, false, MK><<<grid, kThreads2, 0, st>>>(f2);
 }
 
 int64_t s64_of(int Skv) { return (static_cast<int64_t>(Skv) + kStick - 1) / kStick * kStick; }
@@ -764,15 +853,26 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     SPYRE_REQUIRE(static_cast<int64_t>(Skv) * mask_strides[3] < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
                   "mask row spans 2^31 elements or more");
   }
-  // Only the masked kernel reads V through the workspace (V with its sticks
-  // along tokens); calls without a mask need none.
+  // fp16 and bool masks whose rows are whole 16-byte units (keys contiguous,
+  // 16-byte aligned slices) are staged through LDS by the main kernel; any
+  // other mask goes to the per-wavefront kernel, which reads V through the
+  // workspace (V with its sticks along tokens).  Masked calls pass the
+  // workspace either way, calls without a mask need none.
+  int64_t m_span = 0;
+  bool lds_path = mask_kind == kNoMask;
+  if (mask_kind == kMaskF16 || mask_kind == kMaskBool) {
+    const int64_t esz = mask_kind == kMaskF16 ? 2 : 1;
+    m_span = Sq > 0 && Skv > 0 ? ((static_cast<int64_t>(Sq) - 1) * mask_strides[2] + Skv) * esz : 0;
+    lds_path = mask_strides[3] == 1 && aligned16(attn_mask) && (mask_strides[0] * esz) % 16 == 0 &&
+               (mask_strides[1] * esz) % 16 == 0 && (mask_strides[2] * esz) % 16 == 0 && m_span <= kBufRange;
+  }
   const size_t need = mask_kind != kNoMask ? spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D) : 0;
   SPYRE_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
                 SPYRE_ENOSPC, "workspace %zu < %zu bytes (or misaligned)", workspace_bytes, need);
   if (Sq == 0) return SPYRE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int s64 = static_cast<int>(s64_of(Skv));
-  if (Skv > 0 && mask_kind != kNoMask) {
+  if (Skv > 0 && !lds_path) {
     VtArgs va{static_cast<const _Float16*>(v), v_strides[0], v_strides[1], v_strides[2],
               static_cast<_Float16*>(workspace), Hkv, Skv, s64, D,
               static_cast<int64_t>(B) * Hkv * (s64 / 64) * (D / 64)};
@@ -821,8 +921,8 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
   fa.s64 = s64;
   fa.causal = is_causal ? 1 : 0;
   fa.scale_log2 = scale * kLog2e;
-  if (mask_kind == kNoMask) {
-    // K/V tiles shared through LDS.
+  if (lds_path) {
+    // K/V tiles (and mask blocks) shared through LDS.
     Fwd2Args f2{};
     f2.q = fa.q;
     f2.k = fa.k;
@@ -853,14 +953,19 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.scale_log2 = fa.scale_log2;
     // |scale log2 e| <= 1: q times it stays within fp16, so Q is prescaled.
     const bool prescaled = fabsf(f2.scale_log2) <= 1.f;
-    if (D == 128 && prescaled)
-      sdpa_fwd_lds_kernel<128, true><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
-    else if (D == 128)
-      sdpa_fwd_lds_kernel<128, false><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
-    else if (prescaled)
-      sdpa_fwd_lds_kernel<64, true><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+    f2.mask = attn_mask;
+    if (mask_kind != kNoMask) {
+      f2.m_sb = mask_strides[0];
+      f2.m_sh = mask_strides[1];
+      f2.m_sq = mask_strides[2];
+      f2.m_bytes = static_cast<uint32_t>(m_span);
+    }
+    if (mask_kind == kMaskF16)
+      launch_lds<kMaskF16>(f2, D, prescaled, st);
+    else if (mask_kind == kMaskBool)
+      launch_lds<kMaskBool>(f2, D, prescaled, st);
     else
-      sdpa_fwd_lds_kernel<64, false><<<dim3(f2.n_items), kThreads2, 0, st>>>(f2);
+      launch_lds<kNoMask>(f2, D, prescaled, st);
   } else {
     const dim3 grid((Sq + kWaves * kQ - 1) / (kWaves * kQ), Hq, B);
     auto launch = [&](auto mk) {

@@ -92,7 +92,8 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
     s = 1.0 / math.sqrt(D) if scale is None else float(scale)
     out = torch.empty((B, Sq, Hq, D), dtype=torch.float16, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
-    # Only masked calls read V through the workspace.
+    # Masked calls pass a workspace: masks the main kernel cannot stage (fp32,
+    # or rows not whole 16-byte units) run a kernel that reads V through it.
     need = workspace_bytes(B, Hkv, Skv, D) if kind != MASK_NONE else 0
     if workspace is None and need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
