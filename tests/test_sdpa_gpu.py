@@ -179,6 +179,29 @@ def test_staged_mask_fully_masked_rows(cuda, kind):
     assert torch.isinf(lse[:, :, dead]).all() and (lse[:, :, dead] < 0).all()
 
 
+@pytest.mark.parametrize("pattern", ["causal_inf", "causal_min", "window_bool", "padding_bool"])
+def test_block_sparse_masks(cuda, pattern):
+    """Masks that blank whole 32-query x 64-key blocks (causal as a bias of
+    -inf or of fp16's minimum, a sliding window, key padding): such blocks
+    add nothing and are skipped, the rest must still match."""
+    Sq = Skv = 448
+    q = randn((1, 4, Sq, 128), SEED + 23)
+    k, v = randn((1, 2, Skv, 128), SEED + 24), randn((1, 2, Skv, 128), SEED + 25)
+    i = torch.arange(Sq)[:, None]
+    j = torch.arange(Skv)[None, :]
+    if pattern.startswith("causal"):
+        fill = -float("inf") if pattern == "causal_inf" else -65504.0
+        mask = torch.zeros((Sq, Skv)).masked_fill(j > i, fill).half()
+    elif pattern == "window_bool":
+        mask = (j <= i) & (j > i - 100)
+    else:
+        mask = (j < 200).expand(Sq, Skv)
+    out, lse = run(cuda, q, k, v, attn_mask=mask, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, attn_mask=mask.numpy(), return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
 def test_fully_masked_rows_give_zeros_and_minus_inf_lse(cuda):
     q, k, v = randn((1, 2, 40, 64), SEED + 5), randn((1, 2, 33, 64), SEED + 6), randn((1, 2, 33, 64), SEED + 7)
     mask = torch.zeros((40, 33))

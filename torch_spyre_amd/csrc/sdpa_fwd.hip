@@ -613,13 +613,17 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // PRESCALED: s holds exponents relative to m_use, and so does `ahead`
   // (the first half of the next step's scores, computed before this
   // update); a move of m_use shifts both, and the tile.
-  auto update_max = [&](f32x16 (&s)[2], f32x16& ahead) {
+  // The step's row max in the units of m_run.
+  auto row_max = [&](const f32x16 (&s)[2]) {
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[mt][rr]);
-    mx = PRESCALED ? max_xor32(mx) + m_use : max_xor32(mx) * scale_abs;
+    return PRESCALED ? max_xor32(mx) + m_use : max_xor32(mx) * scale_abs;
+  };
+  // ahead2: with a mask, the second half of S(t+1) is complete too.
+  auto update_max = [&](f32x16 (&s)[2], f32x16& ahead, f32x16* ahead2, float mx) {
     if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
@@ -636,6 +640,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
           s[0][rr] -= d;
           s[1][rr] -= d;
           ahead[rr] -= d;
+          if (ahead2) (*ahead2)[rr] -= d;
           neg_m_tile[rr] = -m_use;
         }
       }
@@ -724,32 +729,66 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[i], b, acc, 0, 0, 0);
         if (i + kPrefetch < kNF) fr[i + kPrefetch] = frag(k1, i + kPrefetch);
       };
-      apply_mask(t, cur);
-      if (edge(t)) mask_step(t, cur);
-      nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
+      if constexpr (MK == kNoMask) {
+        if (edge(t)) mask_step(t, cur);
+        nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < DK; ++ks) mfma(ks, qv[ks], nxt[0]);
-      interleave_reads(0, DK);
-      update_max(cur, nxt[0]);
-      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
-      f16x8 p0[2], p1[2];
-      nxt[1] = PRESCALED ? neg_m_tile : f32x16{};
+        for (int ks = 0; ks < DK; ++ks) mfma(ks, qv[ks], nxt[0]);
+        interleave_reads(0, DK);
+        update_max(cur, nxt[0], nullptr, row_max(cur));
+        const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+        f16x8 p0[2], p1[2];
+        nxt[1] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < DK; ++ks) mfma(DK + ks, qv[ks], nxt[1]);
-      softmax_half(cur[0], neg_m, p0);
-      interleave_reads(DK, 2 * DK);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int ks = 0; ks < DK; ++ks) mfma(DK + ks, qv[ks], nxt[1]);
+        softmax_half(cur[0], neg_m, p0);
+        interleave_reads(DK, 2 * DK);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
-      softmax_half(cur[1], neg_m, p1);
-      interleave_reads(2 * DK, 2 * DK + 2 * DM);
-      __builtin_amdgcn_sched_barrier(0);
+          for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
+        softmax_half(cur[1], neg_m, p1);
+        interleave_reads(2 * DK, 2 * DK + 2 * DM);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + 2 * DM + j * DM + dm, p1[j], o[dm]);
+          for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + 2 * DM + j * DM + dm, p1[j], o[dm]);
+      } else {
+        // A mask can leave a step nothing to add: every score of the
+        // wavefront's block -inf or more than 32 below its row's running
+        // max, so every P rounds to 0 in fp16.  Such a step computes only
+        // S(t+1); S(t+1) is therefore computed whole before the softmax.
+        apply_mask(t, cur);
+        if (edge(t)) mask_step(t, cur);
+        const float mx = row_max(cur);
+        const bool live = __builtin_amdgcn_ballot_w64(mx > -INFINITY && mx >= m_run - 32.f) != 0;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          nxt[h2] = PRESCALED ? neg_m_tile : f32x16{};
+#pragma unroll
+          for (int ks = 0; ks < DK; ++ks) mfma(h2 * DK + ks, qv[ks], nxt[h2]);
+        }
+        interleave_reads(0, 2 * DK);
+        if (live) {
+          update_max(cur, nxt[0], &nxt[1], mx);
+          const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+          f16x8 p0[2], p1[2];
+          softmax_half(cur[0], neg_m, p0);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
+          softmax_half(cur[1], neg_m, p1);
+          interleave_reads(2 * DK, 2 * DK + 2 * DM);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + 2 * DM + j * DM + dm, p1[j], o[dm]);
+        }
+      }
     }
     dma_wait();
     __syncthreads();
