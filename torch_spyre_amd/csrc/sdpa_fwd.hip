@@ -10,20 +10,33 @@
 // whose keys are all masked gives zeros and LSE -inf (torch's CPU result;
 // the reference's torch.softmax would give NaN there).
 //
-// Two kernels on the caller's stream:
-//  1. v_token_sticks_kernel: V [B, Hkv, Skv, D] (rows may be strided) ->
-//     Vt [B, Hkv, D, S64] in the workspace: V with its sticks along tokens
-//     (the transpose-restick of each head), zero-padded to S64 = ceil(Skv /
-//     64) * 64.  This makes the PV product's reduction dim (keys) contiguous,
-//     as the paged decode cache stores V.
-//  2. sdpa_fwd_kernel: one wavefront per 32 queries of one (sequence, q
-//     head), four per workgroup, streaming 64 keys per step:
-//       S^T[key, q] = K[key, :] Q^T[:, q]   4 x D/32 x 2 MFMA 16x16x32
-//       online softmax in fp32 (exp2 domain) per query column;
-//       O^T[d, q] += Vt[d, key] P^T[key, q]   D/16 x 2 x 2 MFMA 16x16x32
-//     The keys of the S rows are permuted so that each lane's P values are
-//     the 8 consecutive keys the PV operand needs (no lane exchange).
-//     Causal attention stops each wavefront at its last query's key.
+// Kernels, on the caller's stream:
+//  * sdpa_fwd_lds_kernel serves calls without a mask (plain or causal) and
+//    fp16 / boolean masks whose rows are whole 16-byte units.  A workgroup
+//    of 8 wavefronts takes 256 queries of one (sequence, q head); wavefront w
+//    takes 32.  Per 64-key step the K and V tiles (row-major, padded) move
+//    from L2 straight into LDS (buffer loads with the LDS flag), once for all
+//    8 wavefronts:
+//       S^T[key, q] = K[key, :] Q^T[:, q]     2 x D/16 MFMA 32x32x16
+//       online softmax in fp32 (exp2 domain), lazy rescaling of the max;
+//       O^T[d, q] += V^T[d, key] P^T[key, q]  4 x D/32 MFMA 32x32x16
+//    with the V^T operands read from the row-major V tile by transposing
+//    LDS reads.  The loop is software-pipelined: step t's softmax overlaps
+//    S(t+1).  A mask is staged per wavefront beside the tiles, a step ahead;
+//    steps it blanks for the whole wavefront skip their softmax and P V.
+//  * Other masks (fp32 biases, rows that are not whole 16-byte units):
+//    1. v_token_sticks_kernel: V [B, Hkv, Skv, D] (rows may be strided) ->
+//       Vt [B, Hkv, D, S64] in the workspace: V with its sticks along tokens
+//       (the transpose-restick of each head), zero-padded to S64 = ceil(Skv
+//       / 64) * 64, so the PV product's reduction dim (keys) is contiguous.
+//    2. sdpa_fwd_kernel: one wavefront per 32 queries of one (sequence, q
+//       head), four per workgroup, streaming 64 keys per step from L2:
+//         S^T[key, q] = K[key, :] Q^T[:, q]   4 x D/32 x 2 MFMA 16x16x32
+//         O^T[d, q] += Vt[d, key] P^T[key, q]   D/16 x 2 x 2 MFMA 16x16x32
+//       reading the mask element by element through its broadcast strides.
+// In both, the keys of the S rows are permuted so that each lane's P values
+// are the 8 consecutive keys the PV operand needs (no lane exchange), and
+// causal attention stops each wavefront at its last query's key.
 
 #include <hip/hip_runtime.h>
 
