@@ -197,14 +197,26 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
 #define SPYRE_MASK_F32 2  /* additive fp32 bias                */
 #define SPYRE_MASK_BOOL 3 /* uint8/bool: nonzero = attend      */
 
-/* Workspace bytes needed by spyre_sdpa_fwd_f16 with an attention mask: V
- * re-laid out with its sticks along tokens, B * Hkv * D * ceil(Skv / 64) * 64
- * fp16.  Calls without a mask (plain or causal) need no workspace: they read
- * V as it lies.  So do, in fact, fp16 and bool masks with key stride 1, a
- * 16-byte aligned pointer and b / h / i strides of whole 16 bytes (staged in
- * LDS beside K and V); masked calls pass the workspace all the same, since
- * any other mask (fp32, unaligned) runs a kernel that reads V through it. */
+/* Workspace bytes that cover any spyre_sdpa_fwd_f16 call with an attention
+ * mask: V re-laid out with its sticks along tokens, B * Hkv * D *
+ * ceil(Skv / 64) * 64 fp16, which the fp32-mask kernel reads.  Calls without
+ * a mask (plain or causal) need no workspace. */
 size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
+
+/* The workspace one spyre_sdpa_fwd_f16 call needs, for its mask (same
+ * arguments as the call): 0 without a mask and for fp16 / bool masks with
+ * key stride 1, a 16-byte aligned pointer, b / h / i strides and Skv of
+ * whole 16 bytes (staged in LDS beside K and V as they lie); for other fp16 / bool
+ * masks, a copy with 16-byte rows of the mask's non-broadcast extent (then
+ * staged the same way); for fp32 masks, spyre_sdpa_fwd_workspace_bytes.  A
+ * call whose fp16 / bool mask needs a copy but whose workspace holds only
+ * spyre_sdpa_fwd_workspace_bytes runs the fp32-mask kernel instead (same
+ * results within the SDPA tolerance, slower).  No reference counterpart:
+ * the reference's decomposition (torch_spyre/_inductor/decompositions.py:
+ * 523-609) allocates its intermediates itself. */
+size_t spyre_sdpa_fwd_call_workspace_bytes(const void* attn_mask, int mask_kind,
+                                           const int64_t* mask_strides, int B, int Hq, int Hkv,
+                                           int Sq, int Skv, int D);
 
 /* Scaled dot-product attention forward (prefill, any Sq):
  *   out[b,h,i,:] = softmax_j(scale * q[b,h,i,:] . k[b,h/g,j,:] + bias[b,h,i,j]) v[b,h/g,j,:]

@@ -149,16 +149,20 @@ def test_masks_staged_in_lds(cuda, kind, shape, D):
 
 
 @pytest.mark.parametrize("kind", ["f16", "bool"])
-def test_staged_mask_ignores_bytes_past_skv(cuda, kind):
-    """A mask that is a view of wider rows: the bytes past Skv in each row
-    (NaN for fp16, keep for bool) belong to no key and change nothing; a
-    large scale (|scale log2 e| > 1) takes the unscaled-score form."""
-    Sq, Skv, D = 70, 96, 128
+@pytest.mark.parametrize("Skv", [96, 100])
+def test_staged_mask_ignores_bytes_past_skv(cuda, kind, Skv):
+    """A mask that is a view of wider rows (112 elements): the bytes past Skv
+    in each row (NaN for fp16, keep for bool) belong to no key and change
+    nothing.  Skv 100: rows end inside a 16-byte unit, so the last row's
+    last keys must still count (regression: staged as it lay, that unit
+    arrived as zeros).  A large scale (|scale log2 e| > 1) takes the
+    unscaled-score form."""
+    Sq, D, W = 70, 128, 112
     q, k, v = randn((1, 4, Sq, D), SEED + 15), randn((1, 4, Skv, D), SEED + 16), randn((1, 4, Skv, D), SEED + 17)
-    wide = _mask(kind, (Sq, Skv + 32), SEED + 18)
+    wide = _mask(kind, (Sq, W), SEED + 18)
     wide[:, Skv:] = True if kind == "bool" else float("nan")
     mask = wide.to(cuda)[:, :Skv]  # sliced on the device, so its rows keep their stride
-    assert mask.stride() == (Skv + 32, 1)
+    assert mask.stride() == (W, 1)
     for scale in (None, 2.0):
         out = run(cuda, q, k, v, attn_mask=mask, scale=scale)
         assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask.cpu().contiguous(), scale=scale))
@@ -177,6 +181,52 @@ def test_staged_mask_fully_masked_rows(cuda, kind):
     assert_close(out, OA.sdpa_cpu_fp32(q, k, v, attn_mask=mask))
     assert not out[:, :, dead].float().abs().sum()
     assert torch.isinf(lse[:, :, dead]).all() and (lse[:, :, dead] < 0).all()
+
+
+@pytest.mark.parametrize("kind", ["f16", "bool"])
+@pytest.mark.parametrize("shape", ["qk", "b1qk", "1h1k", "bhqk", "kq_view"])
+def test_unaligned_masks_are_copied(cuda, kind, shape):
+    """fp16 / bool masks whose rows are not whole 16-byte units (Skv 77, a
+    transposed view) are copied with 16-byte rows into the workspace and
+    staged like aligned ones: the output equals, bit for bit, the call with
+    the same mask stored in aligned rows, and matches the oracle."""
+    import torch_spyre_amd as tsa
+
+    B, Hq, Hkv, Sq, Skv, D = 2, 4, 2, 50, 77, 128
+    q = randn((B, Hq, Sq, D), SEED + 26).to(cuda)
+    k, v = randn((B, Hkv, Skv, D), SEED + 27).to(cuda), randn((B, Hkv, Skv, D), SEED + 28).to(cuda)
+    dims = {"qk": (Sq, Skv), "b1qk": (B, 1, Sq, Skv), "1h1k": (1, Hq, 1, Skv), "bhqk": (B, Hq, Sq, Skv),
+            "kq_view": (Skv, Sq)}[shape]
+    mask = _mask(kind, dims, SEED + 29)
+    mask = mask.to(cuda).t() if shape == "kq_view" else mask.to(cuda)  # kq_view: key stride Sq
+    wide = torch.zeros((*mask.shape[:-1], 80), dtype=mask.dtype, device=cuda)
+    wide[..., :Skv] = mask
+    aligned = wide[..., :Skv]  # 160- / 80-byte rows: staged as it lies
+    out = tsa.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)
+    ref = tsa.scaled_dot_product_attention(q, k, v, attn_mask=aligned, enable_gqa=True)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert_close(out, OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), attn_mask=mask.cpu()))
+
+
+def test_unaligned_mask_with_v_sized_workspace(cuda):
+    """A caller's workspace sized for V's relayout but too small for the
+    mask's copy: the call runs the per-wavefront kernel, same results."""
+    import torch_spyre_amd as tsa
+
+    B, Hq, Hkv, Sq, Skv, D = 1, 8, 2, 300, 77, 128
+    q = randn((B, Hq, Sq, D), SEED + 30).to(cuda)
+    k, v = randn((B, Hkv, Skv, D), SEED + 31).to(cuda), randn((B, Hkv, Skv, D), SEED + 32).to(cuda)
+    mask = _mask("f16", (B, Hq, Sq, Skv), SEED + 33).to(cuda)
+    vt = tsa.sdpa.workspace_bytes(B, Hkv, Skv, D)
+    m = mask.expand(B, Hq, Sq, Skv)
+    from torch_spyre_amd import _lib
+
+    need = _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(m.data_ptr(), 1, _lib.i64_array(m.stride()), B, Hq, Hkv,
+                                                          Sq, Skv, D)
+    assert need == B * Hq * Sq * 160 > vt
+    ws = torch.empty(vt, dtype=torch.uint8, device=cuda)
+    out = tsa.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True, workspace=ws)
+    assert_close(out, OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), attn_mask=mask.cpu()))
 
 
 @pytest.mark.parametrize("pattern", ["causal_inf", "causal_min", "window_bool", "padding_bool"])

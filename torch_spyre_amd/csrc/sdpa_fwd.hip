@@ -861,6 +861,103 @@ void launch_lds(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
     sdpa_fwd_lds_kernel<64, false, MK><<<grid, kThreads2, 0, st>>>(f2);
 }
 
+// A copy of a mask with 16-byte rows: [bm][hm][qm][pitch bytes], keys past
+// Skv zero.  One work-item per 16-byte unit; the source is read element by
+// element through its strides (any alignment of its rows).
+struct MaskPadArgs {
+  const char* src;
+  char* dst;
+  int64_t sb, sh, sq, sk;  // source strides, elements
+  int64_t n_units;         // bm * hm * qm * units
+  int hm, qm, units, Skv, esz;
+};
+
+__global__ __launch_bounds__(256) void mask_pad_kernel(MaskPadArgs a) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= a.n_units) return;
+  const int64_t row = u / a.units;
+  const int cu = static_cast<int>(u - row * a.units);
+  const int q = static_cast<int>(row % a.qm);
+  const int64_t bh = row / a.qm;
+  const int h = static_cast<int>(bh % a.hm);
+  const int64_t b = bh / a.hm;
+  const int64_t base = b * a.sb + h * a.sh + q * a.sq;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  if (a.esz == 2) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(a.src);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = cu * 8 + e;
+      const uint32_t x = key < a.Skv ? src[base + key * a.sk] : 0u;
+      w[e >> 1] |= x << (16 * (e & 1));
+    }
+  } else {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.src);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = cu * 16 + e;
+      const uint32_t x = key < a.Skv ? src[base + key * a.sk] : 0u;
+      w[e >> 2] |= x << (8 * (e & 3));
+    }
+  }
+  *reinterpret_cast<uint4*>(a.dst + u * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+bool aligned16(const void* p);
+
+// How a call's mask reaches the kernels:
+//  kRouteNone    no mask;
+//  kRouteStaged  fp16 / bool, rows of whole 16-byte units: the main kernel
+//                stages it as it lies;
+//  kRouteCopied  other fp16 / bool masks: copied with 16-byte rows into the
+//                workspace first (mask_pad_kernel), then staged;
+//  kRouteVt      fp32 masks (or a copy whose slice would pass 2 GiB): the
+//                per-wavefront kernel, V through the workspace.
+enum MaskRoute { kRouteNone, kRouteStaged, kRouteCopied, kRouteVt };
+
+struct MaskPlan {
+  MaskRoute route = kRouteNone;
+  int64_t span = 0;                      // bytes of one (sequence, head) slice as staged
+  int64_t bm = 1, hm = 1, qm = 1, pitch = 0;  // kRouteCopied: extents kept, row pitch (bytes)
+  size_t copy_bytes = 0;
+};
+
+MaskPlan plan_mask(const void* mask, int kind, const int64_t* ms, int B, int Hq, int Sq, int Skv) {
+  MaskPlan p;
+  if (kind == kNoMask) return p;
+  if (kind == kMaskF32) {
+    p.route = kRouteVt;
+    return p;
+  }
+  const int64_t esz = kind == kMaskF16 ? 2 : 1;
+  if (Sq == 0 || Skv == 0) {  // nothing of the mask is read
+    p.route = kRouteStaged;
+    return p;
+  }
+  // Staged as it lies only if every slice ends on a whole 16-byte unit: the
+  // kernel loads whole units and the descriptor's range ends with the slice,
+  // so a unit straddling the end would arrive as zeros, valid keys included.
+  const int64_t span = ((static_cast<int64_t>(Sq) - 1) * ms[2] + Skv) * esz;
+  if (ms[3] == 1 && aligned16(mask) && (ms[0] * esz) % 16 == 0 && (ms[1] * esz) % 16 == 0 &&
+      (ms[2] * esz) % 16 == 0 && (Skv * esz) % 16 == 0 && span <= kBufRange) {
+    p.route = kRouteStaged;
+    p.span = span;
+    return p;
+  }
+  p.bm = ms[0] != 0 ? B : 1;
+  p.hm = ms[1] != 0 ? Hq : 1;
+  p.qm = ms[2] != 0 ? Sq : 1;
+  p.pitch = (static_cast<int64_t>(Skv) * esz + 15) / 16 * 16;
+  p.span = p.qm * p.pitch;  // whole rows: the copy holds the last row's padding
+  if (p.span > kBufRange) {
+    p.route = kRouteVt;
+    return p;
+  }
+  p.route = kRouteCopied;
+  p.copy_bytes = static_cast<size_t>(p.bm * p.hm * p.qm * p.pitch);
+  return p;
+}
+
 int64_t s64_of(int Skv) { return (static_cast<int64_t>(Skv) + kStick - 1) / kStick * kStick; }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -870,6 +967,16 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 extern "C" size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D) {
   if (B <= 0 || Hkv <= 0 || Skv < 0 || D <= 0) return 0;
   return static_cast<size_t>(B) * Hkv * D * s64_of(Skv) * sizeof(_Float16);
+}
+
+extern "C" size_t spyre_sdpa_fwd_call_workspace_bytes(const void* attn_mask, int mask_kind,
+                                                      const int64_t* mask_strides, int B, int Hq, int Hkv,
+                                                      int Sq, int Skv, int D) {
+  if (mask_kind == kNoMask || !mask_strides || mask_kind < kNoMask || mask_kind > kMaskBool) return 0;
+  if (B <= 0 || Hq <= 0 || Sq < 0 || Skv < 0) return 0;
+  const MaskPlan mp = plan_mask(attn_mask, mask_kind, mask_strides, B, Hq, Sq, Skv);
+  if (mp.route == kRouteCopied) return mp.copy_bytes;
+  return mp.route == kRouteVt ? spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D) : 0;
 }
 
 extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const void* k,
@@ -905,25 +1012,47 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     SPYRE_REQUIRE(static_cast<int64_t>(Skv) * mask_strides[3] < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
                   "mask row spans 2^31 elements or more");
   }
-  // fp16 and bool masks whose rows are whole 16-byte units (keys contiguous,
-  // 16-byte aligned slices) are staged through LDS by the main kernel; any
-  // other mask goes to the per-wavefront kernel, which reads V through the
-  // workspace (V with its sticks along tokens).  Masked calls pass the
-  // workspace either way, calls without a mask need none.
-  int64_t m_span = 0;
-  bool lds_path = mask_kind == kNoMask;
-  if (mask_kind == kMaskF16 || mask_kind == kMaskBool) {
-    const int64_t esz = mask_kind == kMaskF16 ? 2 : 1;
-    m_span = Sq > 0 && Skv > 0 ? ((static_cast<int64_t>(Sq) - 1) * mask_strides[2] + Skv) * esz : 0;
-    lds_path = mask_strides[3] == 1 && aligned16(attn_mask) && (mask_strides[0] * esz) % 16 == 0 &&
-               (mask_strides[1] * esz) % 16 == 0 && (mask_strides[2] * esz) % 16 == 0 && m_span <= kBufRange;
-  }
-  const size_t need = mask_kind != kNoMask ? spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D) : 0;
+  if (mask_kind != kNoMask)
+    SPYRE_REQUIRE(reinterpret_cast<uintptr_t>(attn_mask) % (mask_kind == kMaskF32 ? 4 : mask_kind == kMaskF16 ? 2 : 1) == 0,
+                  SPYRE_EINVAL, "mask pointer not aligned to its element");
+  // The mask's route (plan_mask); a masked call whose workspace holds V's
+  // relayout but not the mask's copy takes the per-wavefront kernel.
+  MaskPlan mp = plan_mask(attn_mask, mask_kind, mask_strides, B, Hq, Sq, Skv);
+  if (mp.route == kRouteCopied && (!workspace || workspace_bytes < mp.copy_bytes || !aligned16(workspace)))
+    mp.route = kRouteVt;
+  const size_t need = mp.route == kRouteVt       ? spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D)
+                      : mp.route == kRouteCopied ? mp.copy_bytes
+                                                 : 0;
   SPYRE_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
                 SPYRE_ENOSPC, "workspace %zu < %zu bytes (or misaligned)", workspace_bytes, need);
+  const bool lds_path = mp.route != kRouteVt;
   if (Sq == 0) return SPYRE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int s64 = static_cast<int>(s64_of(Skv));
+  const void* mask_ptr = attn_mask;
+  int64_t m_sb = 0, m_sh = 0, m_sq = 0;
+  if (mask_kind != kNoMask) {
+    m_sb = mask_strides[0];
+    m_sh = mask_strides[1];
+    m_sq = mask_strides[2];
+  }
+  if (mp.route == kRouteCopied) {
+    const int esz = mask_kind == kMaskF16 ? 2 : 1;
+    MaskPadArgs pa{static_cast<const char*>(attn_mask), static_cast<char*>(workspace), mask_strides[0],
+                   mask_strides[1], mask_strides[2], mask_strides[3],
+                   static_cast<int64_t>(mp.copy_bytes / 16), static_cast<int>(mp.hm), static_cast<int>(mp.qm),
+                   static_cast<int>(mp.pitch / 16), Skv, esz};
+    const int64_t blocks = (pa.n_units + 255) / 256;
+    SPYRE_REQUIRE(blocks < (int64_t{1} << 31), SPYRE_EUNSUPPORTED, "mask too large");
+    mask_pad_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, st>>>(pa);
+    const hipError_t e = hipGetLastError();
+    SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "mask copy launch failed: %s", hipGetErrorString(e));
+    const int64_t pe = mp.pitch / esz;  // row pitch, elements
+    mask_ptr = workspace;
+    m_sq = mp.qm > 1 ? pe : 0;
+    m_sh = mp.hm > 1 ? mp.qm * pe : 0;
+    m_sb = mp.bm > 1 ? mp.hm * mp.qm * pe : 0;
+  }
   if (Skv > 0 && !lds_path) {
     VtArgs va{static_cast<const _Float16*>(v), v_strides[0], v_strides[1], v_strides[2],
               static_cast<_Float16*>(workspace), Hkv, Skv, s64, D,
@@ -1005,13 +1134,11 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.scale_log2 = fa.scale_log2;
     // |scale log2 e| <= 1: q times it stays within fp16, so Q is prescaled.
     const bool prescaled = fabsf(f2.scale_log2) <= 1.f;
-    f2.mask = attn_mask;
-    if (mask_kind != kNoMask) {
-      f2.m_sb = mask_strides[0];
-      f2.m_sh = mask_strides[1];
-      f2.m_sq = mask_strides[2];
-      f2.m_bytes = static_cast<uint32_t>(m_span);
-    }
+    f2.mask = mask_ptr;
+    f2.m_sb = m_sb;
+    f2.m_sh = m_sh;
+    f2.m_sq = m_sq;
+    f2.m_bytes = static_cast<uint32_t>(mp.span);
     if (mask_kind == kMaskF16)
       launch_lds<kMaskF16>(f2, D, prescaled, st);
     else if (mask_kind == kMaskBool)
