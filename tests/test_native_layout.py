@@ -172,3 +172,37 @@ def test_invalid_arguments_raise(tsa):
         tsa.SpyreTensorLayout([4, 4], torch.float64)
     assert tsa.get_device_dtype(torch.float64) == tsa.DataFormats.INVALID
     assert tsa.get_device_dtype(torch.bfloat16) == tsa.DataFormats.SEN169_FP16
+
+
+def test_sdpa_call_workspace_routes(tsa):
+    """The per-call SDPA workspace size (host code): none without a mask or
+    for fp16 / bool masks whose slices are whole 16-byte units; a copy with
+    16-byte rows of the non-broadcast extent for other fp16 / bool masks;
+    V's token-stick relayout for fp32 masks."""
+    from torch_spyre_amd import _lib
+
+    L = _lib.lib()
+    B, Hq, Hkv, Sq, D = 2, 8, 2, 100, 128
+
+    def need(kind, strides, Skv, ptr=0x10000):
+        return L.spyre_sdpa_fwd_call_workspace_bytes(ptr, kind, _lib.i64_array(strides), B, Hq, Hkv, Sq, Skv, D)
+
+    vt = L.spyre_sdpa_fwd_workspace_bytes(B, Hkv, 160, D)
+    assert vt == B * Hkv * D * 192 * 2
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, Sq, 160, D) == 0
+    # staged as they lie: fp16 rows of 160 keys (320 B), bool rows of 160 B, broadcasts, wider rows
+    assert need(1, [0, 0, 160, 1], 160) == 0
+    assert need(3, [0, 0, 160, 1], 160) == 0
+    assert need(1, [8 * 100 * 168, 100 * 168, 168, 1], 160) == 0
+    assert need(1, [0, 160, 0, 1], 160) == 0
+    # a misaligned pointer, or a slice that ends inside a 16-byte unit: copied
+    assert need(1, [0, 0, 160, 1], 160, ptr=0x10002) == 100 * 320
+    assert need(1, [0, 0, 168, 1], 164) == 100 * 336  # 164 keys = 328 B -> rows of 336
+    # odd rows: [Sq, 77] fp16 -> 160-B rows; [B, 1, Sq, 77] bool -> 80-B rows, per sequence
+    assert need(1, [0, 0, 77, 1], 77) == 100 * 160
+    assert need(3, [100 * 77, 0, 77, 1], 77) == B * 100 * 80
+    # a padding row [1, Hq, 1, 77] and a transposed view (key stride Sq)
+    assert need(1, [0, 77, 0, 1], 77) == Hq * 160
+    assert need(1, [0, 0, 1, 100], 77) == 100 * 160
+    # fp32 masks take V's relayout
+    assert need(2, [0, 0, 160, 1], 160) == vt
