@@ -1011,10 +1011,10 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
       SPYRE_REQUIRE(mask_strides[i] >= 0, SPYRE_EINVAL, "negative mask stride");
     SPYRE_REQUIRE(static_cast<int64_t>(Skv) * mask_strides[3] < (int64_t{1} << 31), SPYRE_EUNSUPPORTED,
                   "mask row spans 2^31 elements or more");
+    const uintptr_t esz = mask_kind == kMaskF32 ? 4 : mask_kind == kMaskF16 ? 2 : 1;
+    SPYRE_REQUIRE(reinterpret_cast<uintptr_t>(attn_mask) % esz == 0, SPYRE_EINVAL,
+                  "mask pointer not aligned to its element");
   }
-  if (mask_kind != kNoMask)
-    SPYRE_REQUIRE(reinterpret_cast<uintptr_t>(attn_mask) % (mask_kind == kMaskF32 ? 4 : mask_kind == kMaskF16 ? 2 : 1) == 0,
-                  SPYRE_EINVAL, "mask pointer not aligned to its element");
   // The mask's route (plan_mask); a masked call whose workspace holds V's
   // relayout but not the mask's copy takes the per-wavefront kernel.
   MaskPlan mp = plan_mask(attn_mask, mask_kind, mask_strides, B, Hq, Sq, Skv);
