@@ -12,7 +12,8 @@ two KV caches (1.07 GB) alternate so the 256 MB last-level cache cannot
 serve a step from the previous one.
 
 Also timed: under "more_configs", the dense MHA decode call (q [1, 8, 1, 64], k/v
-[1, 8, 512, 64]; absolute µs, launch-bound), the ragged batch (64 sequences, context
+[1, 8, 512, 64]; absolute µs, launch-bound), the Llama-3-8B decode step through SDPA
+with dense K/V (q [32, 32, 1, 128], k/v [32, 8, 4096, 128]), the ragged batch (64 sequences, context
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
 heads, append one token at position 131072, attend over 131073 tokens) and
 prefill SDPA, causal, full and with an fp16 / boolean [4096, 4096] mask
@@ -164,6 +165,18 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     ms = timed(lambda i: tsa.sdpa_decode(q1, k1, v1, scale=0.125), steps, warmup, stream)
     res["dense_mha_decode_b1_h8_s512_d64"] = {"us_per_call": round(ms * 1e3, 2),
                                                "algorithmic_bytes": 1_050_624}
+    # the Llama-3-8B decode step through SDPA with dense (unpaged) K/V:
+    # q [32, 32, 1, 128], k/v [32, 8, 4096, 128] (the q heads of a KV head
+    # packed into one block's rows)
+    q2 = torch.randn((32, HQ, 1, D), generator=gg, device=dev).half()
+    k2 = torch.randn((32, HKV, 4096, D), generator=gg, device=dev).half()
+    v2 = torch.randn((32, HKV, 4096, D), generator=gg, device=dev).half()
+    ms = timed(lambda i: tsa.scaled_dot_product_attention(q2, k2, v2, enable_gqa=True), steps, warmup, stream)
+    nb = 2 * k2.numel() * 2 + 2 * q2.numel() * 2
+    res["dense_gqa_decode_b32_h32_8_s4096"] = {
+        "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+        "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb, "kernels_per_step": 1}
+    del q2, k2, v2
 
     def paged(lens, Hq, Hkv):
         pages = [(c + PAGE - 1) // PAGE for c in lens]

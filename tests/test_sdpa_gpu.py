@@ -105,6 +105,19 @@ def test_gqa_groups(cuda, g):
     assert_close(run(cuda, q, k, v, enable_gqa=True), OA.sdpa_cpu_fp32(q, k, v))
 
 
+@pytest.mark.parametrize("Sq,Skv,causal", [(1, 300, False), (5, 300, False), (33, 70, True), (64, 64, True)])
+def test_gqa_heads_packed_into_rows(cuda, Sq, Skv, causal):
+    """Short query runs without a mask on a grid of 512 (sequence, KV head)
+    pairs: the 4 q heads of a KV head share one block's rows (row = query x 4
+    + head), so decode reads each K / V tile once for the group."""
+    q = randn((64, 32, Sq, 128), SEED + 50 + Sq)
+    k, v = randn((64, 8, Skv, 128), SEED + 51), randn((64, 8, Skv, 128), SEED + 52)
+    out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, is_causal=causal))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, is_causal=causal, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
 @pytest.mark.parametrize("kind", ["f16", "f32", "bool"])
 @pytest.mark.parametrize("shape", ["qk", "b1qk", "1h1k"])
 def test_masks_broadcast(cuda, kind, shape):

@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <type_traits>
 
@@ -400,6 +401,9 @@ struct Fwd2Args {
   _Float16* out;
   float* lse;
   int B, Hq, Hkv, g, Sq, Skv, causal, qblocks;
+  // Rows per query: 1, or (calls without a mask, Sq < 256) the g q heads of
+  // a KV head, which then share each K / V tile; gp = g / pack.
+  int pack, gp;
   uint32_t n_items;
   int xcd_remap;
   float scale_log2;
@@ -436,21 +440,29 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * g + gi: the
   // blocks of one (sequence, KV head) are consecutive, latest query block
   // (longest, under causal masking) first across its g q heads.
+  // With pack > 1 a block's rows are (query, q head) pairs of one KV head,
+  // row = query * pack + head in group.
   uint32_t item = blockIdx.x;
   if (a.xcd_remap) item = (item % 8) * (a.n_items / 8) + item / 8;
-  const int gi = static_cast<int>(item % a.g);
-  uint32_t r = item / a.g;
+  const int pack = MK == kNoMask ? a.pack : 1;
+  const int gi = static_cast<int>(item % a.gp);
+  uint32_t r = item / a.gp;
   const int qb = a.qblocks - 1 - static_cast<int>(r % a.qblocks);
   r /= a.qblocks;
   const int kvh = static_cast<int>(r % a.Hkv);
   const int b = static_cast<int>(r / a.Hkv);
-  const int h = kvh * a.g + gi;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   __builtin_assume(wave >= 0 && wave < kWaves2);  // lets the compiler drop always-true load guards
-  const int qw0 = qb * kQB, q0 = qw0 + wave * kQW;
+  const int qw0 = qb * kQB, q0 = qw0 + wave * kQW;  // rows
   const int col = lane & 31, half = lane >> 5;
-  const int qi = q0 + col;
+  const int qrow = q0 + col;
+  const int qi = pack == 1 ? qrow : qrow / pack;  // this lane's query
+  const int h = kvh * a.g + (pack == 1 ? gi : qrow - qi * pack);
   const bool q_ok = qi < a.Sq;
+  // The wavefront's first and last query, and the block's last.
+  const int q_lo = pack == 1 ? q0 : q0 / pack;
+  const int q_hi = pack == 1 ? q0 + kQW - 1 : (q0 + kQW - 1) / pack;
+  const int qb_hi = pack == 1 ? qw0 + kQB - 1 : (qw0 + kQB - 1) / pack;
 
   // Q^T operand: lane (query column, half) holds features 16ks + 8half .. +8.
   f16x8 qv[DK];
@@ -549,13 +561,13 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // The loads must have landed before the barrier that publishes them.
   auto dma_wait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
-  const int key_end = a.causal ? min(a.Skv, qw0 + kQB) : a.Skv;
+  const int key_end = a.causal ? min(a.Skv, qb_hi + 1) : a.Skv;
   const int n_tiles = (key_end + kKT - 1) / kKT;
   // Step t has work for this wavefront unless all its keys are masked
   // (causal: keys past the wavefront's last query).
-  auto active = [&](int t) { return t < n_tiles && q0 < a.Sq && (!a.causal || t * kKT <= q0 + kQW - 1); };
+  auto active = [&](int t) { return t < n_tiles && q_lo < a.Sq && (!a.causal || t * kKT <= q_hi); };
   // Only steps crossing Skv or the causal diagonal need the key test.
-  auto edge = [&](int t) { return t * kKT + kKT > a.Skv || (a.causal && t * kKT + kKT - 1 > q0); };
+  auto edge = [&](int t) { return t * kKT + kKT > a.Skv || (a.causal && t * kKT + kKT - 1 > q_lo); };
   // |scale| (its sign is folded into Q), kept above 0 so that masked scores
   // (-inf) stay -inf; a scale of 0 then gives the uniform weights it should.
   const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
@@ -958,6 +970,33 @@ MaskPlan plan_mask(const void* mask, int kind, const int64_t* ms, int B, int Hq,
   return p;
 }
 
+// Compute units of the current device, cached per device; 0 if the runtime
+// cannot say.
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 0;
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// Rows per query for a call without a mask: the largest divisor p of g whose
+// packed grid (B Hkv (g / p) ceil(p Sq / 256) blocks) still gives every
+// compute unit a block, so packing never idles units.
+int pack_heads(int B, int Hkv, int g, int Sq) {
+  if (Sq >= kQB || g == 1) return 1;
+  const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+  for (int p = g; p > 1; --p) {
+    if (g % p) continue;
+    const int64_t blocks = static_cast<int64_t>(B) * Hkv * (g / p) * ((static_cast<int64_t>(p) * Sq + kQB - 1) / kQB);
+    if (blocks >= cus) return p;
+  }
+  return 1;
+}
+
 int64_t s64_of(int Skv) { return (static_cast<int64_t>(Skv) + kStick - 1) / kStick * kStick; }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -1126,8 +1165,13 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.Sq = Sq;
     f2.Skv = Skv;
     f2.causal = fa.causal;
-    f2.qblocks = (Sq + kQB - 1) / kQB;
-    const int64_t items = static_cast<int64_t>(B) * Hq * f2.qblocks;
+    // Without a mask, short query runs pack q heads of a KV head into one
+    // block's rows, so they share each K / V tile (decode: one block per
+    // (sequence, KV head) instead of g mostly idle ones).
+    f2.pack = mask_kind == kNoMask ? pack_heads(B, Hkv, fa.g, Sq) : 1;
+    f2.gp = fa.g / f2.pack;
+    f2.qblocks = static_cast<int>((static_cast<int64_t>(f2.pack) * Sq + kQB - 1) / kQB);
+    const int64_t items = static_cast<int64_t>(B) * Hkv * f2.gp * f2.qblocks;
     SPYRE_REQUIRE(items < (int64_t{1} << 31), SPYRE_EUNSUPPORTED, "too many query blocks");
     f2.n_items = static_cast<uint32_t>(items);
     f2.xcd_remap = items % 8 == 0;
