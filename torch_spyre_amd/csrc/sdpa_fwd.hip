@@ -428,14 +428,19 @@ template <> struct MaskTile<kMaskBool> {  // 64 + 16 bytes per row
 // already as exponents: the first QK MFMA starts from a tile holding -m
 // (the running max), so P = exp2(S) needs no per-score FMA.  Otherwise the
 // scale's sign is folded into Q and its magnitude into the exponent's FMA.
-template <int D, bool PRESCALED, int MK>
+// SLOTS: K / V slots in LDS.  Two: each step's tiles are loaded one step
+// ahead, a barrier per step.  Four (calls without a mask whose blocks have
+// fewer than 256 rows, e.g. decode, where one wavefront computes and the
+// step waits on its loads): loads two steps ahead, a barrier per two steps.
+template <int D, bool PRESCALED, int MK, int SLOTS = 2>
 __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
+  static_assert(SLOTS == 2 || (SLOTS == 4 && MK == kNoMask), "four slots leave no room for a mask");
   using L = Lds2<D>;
   using MT = MaskTile<MK>;
   constexpr int DK = D / 16;  // QK k-steps
   constexpr int DM = D / 32;  // O row tiles
   // Two K / V slots, then (masked calls) two mask blocks per wavefront.
-  __shared__ __align__(16) _Float16 lds[2 * L::kSlot + kWaves2 * MT::kBytes];
+  __shared__ __align__(16) _Float16 lds[SLOTS * L::kSlot + kWaves2 * MT::kBytes];
 
   // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * g + gi: the
   // blocks of one (sequence, KV head) are consecutive, latest query block
@@ -549,7 +554,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       m_off[j] = ok ? static_cast<uint32_t>((row * a.m_sq) * MT::kEsz + 16 * ch) : kOob;
     }
   }
-  auto mask_block = [&](int slot) { return lds + 2 * L::kSlot + (slot * kWaves2 + wave) * (MT::kBytes / 2); };
+  auto mask_block = [&](int slot) { return lds + SLOTS * L::kSlot + (slot * kWaves2 + wave) * (MT::kBytes / 2); };
   auto dma_m = [&](int kb, int slot) {
     if constexpr (MK != kNoMask) {
       const uint32_t done = static_cast<uint32_t>(kb) * MT::kEsz;  // < Skv esz <= m_left
@@ -737,14 +742,25 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // wavefront's last active step S(t+1) reads a stale K slot and is never
   // used.
   auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-    const _Float16* k1 = lds + ((t + 1) & 1) * L::kSlot;
-    // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces V(t-1);
-    // both land during this step's math.
-    if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
-    if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
-    if (t + 1 < n_tiles) dma_m((t + 1) * kKT, (t + 1) & 1);
+    const _Float16* k1 = lds + ((t + 1) % SLOTS) * L::kSlot;
+    if constexpr (SLOTS == 2) {
+      // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces
+      // V(t-1); both land during this step's math.
+      if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
+      if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
+      if (t + 1 < n_tiles) dma_m((t + 1) * kKT, (t + 1) & 1);
+    } else if ((t & 1) == 0) {
+      // Steps t, t + 1 read K(t+1), K(t+2), V(t), V(t+1) (slot = tile % 4);
+      // K(t+3), K(t+4), V(t+2), V(t+3) fill the other four slot halves,
+      // whose last readers were steps t - 2 and t - 1, and land by the
+      // barrier after step t + 1.
+      if (t + 3 < n_tiles) dma_k((t + 3) * kKT, (t + 3) % 4);
+      if (t + 4 < n_tiles) dma_k((t + 4) * kKT, t % 4);
+      if (t + 2 < n_tiles) dma_v((t + 2) * kKT, (t + 2) % 4);
+      if (t + 3 < n_tiles) dma_v((t + 3) * kKT, (t + 3) % 4);
+    }
     if (active(t)) {
-      vtr = static_cast<uint32_t>((t & 1) * L::kSlot + L::kK) + vtr_lane;
+      vtr = static_cast<uint32_t>((t % SLOTS) * L::kSlot + L::kK) + vtr_lane;
       asm volatile("" : "+v"(vtr));
       f16x8 fr[kNF];
 #pragma unroll
@@ -815,11 +831,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         }
       }
     }
-    dma_wait();
-    __syncthreads();
+    if (SLOTS == 2 || (t & 1)) {
+      dma_wait();
+      __syncthreads();
+    }
   };
 
-  // Prologue: K(0), V(0) in slot 0 and K(1) in slot 1, then S(0).  A step
+  // Prologue: K(0), V(0) in slot 0 and K(1) in slot 1 (four slots: also
+  // V(1) and K(2)), then S(0).  A step
   // writes nxt only when it is active, and a step is active only if the one
   // before it is, so S is never read unwritten.
   f32x16 sa[2], sb[2];
@@ -829,6 +848,10 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     dma_m(0, 0);
   }
   if (n_tiles > 1) dma_k(kKT, 1);
+  if constexpr (SLOTS == 4) {
+    if (n_tiles > 1) dma_v(kKT, 1);
+    if (n_tiles > 2) dma_k(2 * kKT, 2);
+  }
   dma_wait();
   __syncthreads();
   if (active(0)) {
@@ -860,17 +883,17 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     a.lse[(static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi] = l > 0.f ? (m_run + log2f(l)) * kLn2 : -INFINITY;
 }
 
-template <int MK>
+template <int MK, int SLOTS = 2>
 void launch_lds(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
   const dim3 grid(f2.n_items);
   if (D == 128 && prescaled)
-    sdpa_fwd_lds_kernel<128, true, MK><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<128, true, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
   else if (D == 128)
-    sdpa_fwd_lds_kernel<128, false, MK><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<128, false, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
   else if (prescaled)
-    sdpa_fwd_lds_kernel<64, true, MK><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<64, true, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
   else
-    sdpa_fwd_lds_kernel<64, false, MK><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<64, false, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
 }
 
 // A copy of a mask with 16-byte rows: [bm][hm][qm][pitch bytes], keys past
@@ -1187,6 +1210,8 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
       launch_lds<kMaskF16>(f2, D, prescaled, st);
     else if (mask_kind == kMaskBool)
       launch_lds<kMaskBool>(f2, D, prescaled, st);
+    else if (static_cast<int64_t>(f2.pack) * Sq < kQB)
+      launch_lds<kNoMask, 4>(f2, D, prescaled, st);  // blocks with fewer rows than wavefronts can fill
     else
       launch_lds<kNoMask>(f2, D, prescaled, st);
   } else {
