@@ -203,8 +203,12 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
  * a mask (plain or causal) need no workspace. */
 size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
 
-/* The workspace one spyre_sdpa_fwd_f16 call needs, for its mask (same
- * arguments as the call): 0 without a mask and for fp16 / bool masks with
+/* The workspace one spyre_sdpa_fwd_f16 call needs (same arguments as the
+ * call, less the causal flag).  Without a mask: the fp32 partials of a key
+ * split, B * Hq * Sq * nsplit * (D + 2) * 4 bytes, when the call's blocks
+ * would not fill the device (short query runs, few sequences, long keys);
+ * a call given less (or causal) runs unsplit, same results within the SDPA
+ * tolerance, slower.  With a mask: 0 for fp16 / bool masks with
  * key stride 1, a 16-byte aligned pointer, b / h / i strides and Skv of
  * whole 16 bytes (staged in LDS beside K and V as they lie); for other fp16 / bool
  * masks, a copy with 16-byte rows of the mask's non-broadcast extent (then

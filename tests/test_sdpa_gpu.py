@@ -335,24 +335,51 @@ def test_overrideable_tuple_and_custom_op(cuda):
 
 
 def test_workspace_only_for_masks(cuda):
-    """Calls without a mask read V as it lies (no workspace, none allocated):
-    with and without a caller's workspace the bits agree; K and V with
+    """Calls without a mask read V as it lies: with a caller's workspace of
+    the size the call asks for (a key split's partials here: 16 blocks for
+    the device) the bits equal the call that allocates its own; with none or
+    a smaller one, the unsplit grid runs, within the bar.  K and V with
     different row strides; a masked call still checks its workspace."""
     import torch_spyre_amd as tsa
+    from torch_spyre_amd import _lib
 
     q = randn((1, 8, 300, 128), SEED + 40).to(cuda)
-    k = randn((1, 2, 333, 128), SEED + 41).to(cuda)
-    v = randn((1, 333, 2, 128), SEED + 42).to(cuda).transpose(1, 2)  # row stride 256, K's is 128
+    k = randn((1, 2, 1100, 128), SEED + 41).to(cuda)
+    v = randn((1, 1100, 2, 128), SEED + 42).to(cuda).transpose(1, 2)  # row stride 256, K's is 128
     for causal in (False, True):
+        need = _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 2, 300, 1100, 128)
+        assert need > 0
         a = tsa.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True)
-        ws = torch.empty(tsa.sdpa.workspace_bytes(1, 2, 333, 128), dtype=torch.uint8, device=cuda)
+        ws = torch.empty(max(need, 16), dtype=torch.uint8, device=cuda)
         b = tsa.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True, workspace=ws)
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
-        assert_close(a, OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), is_causal=causal))
-    mask = torch.zeros((300, 333), dtype=torch.float16, device=cuda)
+        c = tsa.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True,
+                                             workspace=torch.empty(16, dtype=torch.uint8, device=cuda))
+        ref = OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), is_causal=causal)
+        assert_close(a, ref)
+        assert_close(c, ref)
+    mask = torch.zeros((300, 1100), dtype=torch.float16, device=cuda)
     with pytest.raises(ValueError):
         tsa.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True,
                                          workspace=torch.empty(16, dtype=torch.uint8, device=cuda))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,D", [(1, 32, 8, 4096, 128), (1, 32, 8, 1500, 128), (1, 8, 8, 2048, 64),
+                                            (2, 64, 8, 3000, 128)])
+def test_key_split_for_small_grids(cuda, B, Hq, Hkv, Skv, D):
+    """Decode with few (sequence, KV head) pairs: the keys are split across
+    blocks so the grid fills the device, and the partials are merged (batch
+    1 decode of the Llama-3-8B shape, a ragged last split, D 64 without
+    GQA, a key count that is no multiple of 64)."""
+    from torch_spyre_amd import _lib
+
+    assert _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, 1, Skv, D) > 0  # split
+    q = randn((B, Hq, 1, D), SEED + 60 + Skv)
+    k, v = randn((B, Hkv, Skv, D), SEED + 61), randn((B, Hkv, Skv, D), SEED + 62)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
 
 
 def test_argument_errors(cuda):

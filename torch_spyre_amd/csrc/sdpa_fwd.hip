@@ -404,6 +404,12 @@ struct Fwd2Args {
   // Rows per query: 1, or (calls without a mask, Sq < 256) the g q heads of
   // a KV head, which then share each K / V tile; gp = g / pack.
   int pack, gp;
+  // Key split (calls without a mask or causal flag whose blocks would not
+  // fill the device): block sp attends keys sp * split_keys .. + split_keys
+  // - 1 and writes its fp32 partial (O, row max, row sum) to part; a merge
+  // pass combines them.  nsplit == 1: no split.
+  int nsplit, split_keys;
+  float* part;
   uint32_t n_items;
   int xcd_remap;
   float scale_log2;
@@ -450,6 +456,8 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   uint32_t item = blockIdx.x;
   if (a.xcd_remap) item = (item % 8) * (a.n_items / 8) + item / 8;
   const int pack = MK == kNoMask ? a.pack : 1;
+  const int sp = MK == kNoMask ? static_cast<int>(item % a.nsplit) : 0;
+  if (MK == kNoMask) item /= a.nsplit;
   const int gi = static_cast<int>(item % a.gp);
   uint32_t r = item / a.gp;
   const int qb = a.qblocks - 1 - static_cast<int>(r % a.qblocks);
@@ -566,13 +574,15 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // The loads must have landed before the barrier that publishes them.
   auto dma_wait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
-  const int key_end = a.causal ? min(a.Skv, qb_hi + 1) : a.Skv;
-  const int n_tiles = (key_end + kKT - 1) / kKT;
+  // This block's keys: kb0 .. key_end - 1 (the whole row unless split).
+  const int kb0 = sp * a.split_keys;
+  const int key_end = a.causal ? min(a.Skv, qb_hi + 1) : (a.nsplit > 1 ? min(a.Skv, kb0 + a.split_keys) : a.Skv);
+  const int n_tiles = (key_end - kb0 + kKT - 1) / kKT;
   // Step t has work for this wavefront unless all its keys are masked
   // (causal: keys past the wavefront's last query).
-  auto active = [&](int t) { return t < n_tiles && q_lo < a.Sq && (!a.causal || t * kKT <= q_hi); };
+  auto active = [&](int t) { return t < n_tiles && q_lo < a.Sq && (!a.causal || kb0 + t * kKT <= q_hi); };
   // Only steps crossing Skv or the causal diagonal need the key test.
-  auto edge = [&](int t) { return t * kKT + kKT > a.Skv || (a.causal && t * kKT + kKT - 1 > q_lo); };
+  auto edge = [&](int t) { return kb0 + t * kKT + kKT > a.Skv || (a.causal && kb0 + t * kKT + kKT - 1 > q_lo); };
   // |scale| (its sign is folded into Q), kept above 0 so that masked scores
   // (-inf) stay -inf; a scale of 0 then gives the uniform weights it should.
   const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
@@ -601,7 +611,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // half (register 4i + v).  Masked scores become -inf.
   const int key_last = a.causal ? min(a.Skv - 1, qi) : a.Skv - 1;  // this lane's last visible key
   auto mask_step = [&](int t, f32x16 (&s)[2]) {
-    const int kl = key_last - t * kKT - 8 * half;  // key32_of adds 8 per lane half
+    const int kl = key_last - (kb0 + t * kKT) - 8 * half;  // key32_of adds 8 per lane half
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -746,18 +756,18 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     if constexpr (SLOTS == 2) {
       // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces
       // V(t-1); both land during this step's math.
-      if (t + 2 < n_tiles) dma_k((t + 2) * kKT, t & 1);
-      if (t + 1 < n_tiles) dma_v((t + 1) * kKT, (t + 1) & 1);
-      if (t + 1 < n_tiles) dma_m((t + 1) * kKT, (t + 1) & 1);
+      if (t + 2 < n_tiles) dma_k(kb0 + (t + 2) * kKT, t & 1);
+      if (t + 1 < n_tiles) dma_v(kb0 + (t + 1) * kKT, (t + 1) & 1);
+      if (t + 1 < n_tiles) dma_m(kb0 + (t + 1) * kKT, (t + 1) & 1);
     } else if ((t & 1) == 0) {
       // Steps t, t + 1 read K(t+1), K(t+2), V(t), V(t+1) (slot = tile % 4);
       // K(t+3), K(t+4), V(t+2), V(t+3) fill the other four slot halves,
       // whose last readers were steps t - 2 and t - 1, and land by the
       // barrier after step t + 1.
-      if (t + 3 < n_tiles) dma_k((t + 3) * kKT, (t + 3) % 4);
-      if (t + 4 < n_tiles) dma_k((t + 4) * kKT, t % 4);
-      if (t + 2 < n_tiles) dma_v((t + 2) * kKT, (t + 2) % 4);
-      if (t + 3 < n_tiles) dma_v((t + 3) * kKT, (t + 3) % 4);
+      if (t + 3 < n_tiles) dma_k(kb0 + (t + 3) * kKT, (t + 3) % 4);
+      if (t + 4 < n_tiles) dma_k(kb0 + (t + 4) * kKT, t % 4);
+      if (t + 2 < n_tiles) dma_v(kb0 + (t + 2) * kKT, (t + 2) % 4);
+      if (t + 3 < n_tiles) dma_v(kb0 + (t + 3) * kKT, (t + 3) % 4);
     }
     if (active(t)) {
       vtr = static_cast<uint32_t>((t % SLOTS) * L::kSlot + L::kK) + vtr_lane;
@@ -843,14 +853,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // before it is, so S is never read unwritten.
   f32x16 sa[2], sb[2];
   if (n_tiles > 0) {
-    dma_k(0, 0);
-    dma_v(0, 0);
-    dma_m(0, 0);
+    dma_k(kb0, 0);
+    dma_v(kb0, 0);
+    dma_m(kb0, 0);
   }
-  if (n_tiles > 1) dma_k(kKT, 1);
+  if (n_tiles > 1) dma_k(kb0 + kKT, 1);
   if constexpr (SLOTS == 4) {
-    if (n_tiles > 1) dma_v(kKT, 1);
-    if (n_tiles > 2) dma_k(2 * kKT, 2);
+    if (n_tiles > 1) dma_v(kb0 + kKT, 1);
+    if (n_tiles > 2) dma_k(kb0 + 2 * kKT, 2);
   }
   dma_wait();
   __syncthreads();
@@ -867,6 +877,23 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 
   const float l = sum_xor32(l_run);
   if (!q_ok) return;
+  if (MK == kNoMask && a.nsplit > 1) {
+    // The partial: O unnormalised (relative to m_run), then m_run and l.
+    const int64_t prow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * a.nsplit + sp;
+    float* po = a.part + prow * D;
+#pragma unroll
+    for (int dm = 0; dm < DM; ++dm)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<f32x4*>(po + 32 * dm + 8 * i + 4 * half) =
+            f32x4{o[dm][4 * i], o[dm][4 * i + 1], o[dm][4 * i + 2], o[dm][4 * i + 3]};
+    if (half == 0) {
+      float* pml = a.part + static_cast<int64_t>(a.B) * a.Hq * a.Sq * a.nsplit * D + 2 * prow;
+      pml[0] = m_run;
+      pml[1] = l;
+    }
+    return;
+  }
   _Float16* op = a.out + ((static_cast<int64_t>(b) * a.Sq + qi) * a.Hq + h) * D;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   // Lane (query column, half) holds O^T rows d = 32dm + 8i + 4half + v.
@@ -881,6 +908,104 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     }
   if (a.lse && half == 0)
     a.lse[(static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi] = l > 0.f ? (m_run + log2f(l)) * kLn2 : -INFINITY;
+}
+
+// Combines a key split's partials per (sequence, q head, query): one
+// work-item per 4 features of a row.  Splits with l = 0 (no visible key)
+// carry no weight; a row with none gives zeros and LSE -inf.
+struct MergeArgs {
+  const float* part;
+  _Float16* out;
+  float* lse;
+  int Hq, Sq, D, nsplit;
+  int64_t rows;  // B * Hq * Sq
+};
+
+__global__ __launch_bounds__(256) void sdpa_split_merge_kernel(MergeArgs a) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int d4 = a.D / 4;
+  if (u >= a.rows * d4) return;
+  const int64_t r = u / d4;
+  const int d = static_cast<int>(u - r * d4) * 4;
+  const float* pml = a.part + a.rows * a.nsplit * a.D + 2 * r * a.nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s)
+    if (pml[2 * s + 1] > 0.f) M = fmaxf(M, pml[2 * s]);
+  float L = 0.f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < a.nsplit; ++s) {
+    const float ls = pml[2 * s + 1];
+    if (!(ls > 0.f)) continue;
+    const float w = exp2f(pml[2 * s] - M);
+    L += ls * w;
+    acc += *reinterpret_cast<const f32x4*>(a.part + (r * a.nsplit + s) * a.D + d) * w;
+  }
+  const int64_t qi = r % a.Sq, bh = r / a.Sq;
+  const int64_t h = bh % a.Hq, b = bh / a.Hq;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  f16x4 rv;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) rv[v] = static_cast<_Float16>(acc[v] * inv);
+  *reinterpret_cast<f16x4*>(a.out + ((b * a.Sq + qi) * a.Hq + h) * a.D + d) = rv;
+  if (a.lse && d == 0) a.lse[r] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+}
+
+int device_cus();
+
+// Key split of a call without a mask or causal flag: splits enough that the
+// grid gives every compute unit a block, each split at least 8 steps (512
+// keys; shorter splits lose more to the merge pass than they gain).
+// Returns nsplit; split_keys is a multiple of 64.
+int plan_split(int64_t blocks, int Skv, int* split_keys) {
+  *split_keys = Skv;
+  const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+  if (blocks >= cus || Skv < 1024) return 1;
+  const int64_t ns = std::min<int64_t>((cus + blocks - 1) / blocks, Skv / 512);
+  if (ns <= 1) return 1;
+  const int64_t keys = ((Skv + ns - 1) / ns + kKT - 1) / kKT * kKT;
+  *split_keys = static_cast<int>(keys);
+  return static_cast<int>((Skv + keys - 1) / keys);
+}
+
+size_t split_bytes(int64_t rows, int nsplit, int D) {
+  return nsplit > 1 ? static_cast<size_t>(rows) * nsplit * (D + 2) * sizeof(float) : 0;
+}
+
+int pack_heads(int B, int Hkv, int g, int Sq);
+
+int64_t blocks_for(int B, int Hkv, int g, int Sq, int pack) {
+  return static_cast<int64_t>(B) * Hkv * (g / pack) * ((static_cast<int64_t>(pack) * Sq + kQB - 1) / kQB);
+}
+
+// The grid of a call without a mask: short query runs pack all g q heads of
+// a KV head into one block's rows and split the keys until the grid fills
+// the device, if the workspace (ws_bytes) holds the split's partials;
+// otherwise the heads are packed only as far as the unsplit grid still
+// fills the device (pack_heads).
+struct GridPlan {
+  int pack = 1, nsplit = 1, split_keys = 0;
+  size_t part_bytes = 0;
+};
+
+GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, size_t ws_bytes) {
+  GridPlan gp;
+  const int g = Hq / Hkv;
+  gp.split_keys = Skv;
+  if (!causal && Sq > 0) {
+    const int p0 = Sq < kQB ? g : 1;
+    int keys = Skv;
+    const int ns = plan_split(blocks_for(B, Hkv, g, Sq, p0), Skv, &keys);
+    const size_t pb = split_bytes(static_cast<int64_t>(B) * Hq * Sq, ns, D);
+    if (ns > 1 && ws_bytes >= pb) {
+      gp.pack = p0;
+      gp.nsplit = ns;
+      gp.split_keys = keys;
+      gp.part_bytes = pb;
+      return gp;
+    }
+  }
+  gp.pack = pack_heads(B, Hkv, g, Sq);
+  return gp;
 }
 
 template <int MK, int SLOTS = 2>
@@ -1034,8 +1159,10 @@ extern "C" size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D)
 extern "C" size_t spyre_sdpa_fwd_call_workspace_bytes(const void* attn_mask, int mask_kind,
                                                       const int64_t* mask_strides, int B, int Hq, int Hkv,
                                                       int Sq, int Skv, int D) {
-  if (mask_kind == kNoMask || !mask_strides || mask_kind < kNoMask || mask_kind > kMaskBool) return 0;
-  if (B <= 0 || Hq <= 0 || Sq < 0 || Skv < 0) return 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Sq < 0 || Skv < 0 || (D != 64 && D != 128)) return 0;
+  if (mask_kind == kNoMask)  // a key split's partials (calls without the causal flag)
+    return plan_grid(B, Hq, Hkv, Sq, Skv, D, false, SIZE_MAX).part_bytes;
+  if (!mask_strides || mask_kind < kNoMask || mask_kind > kMaskBool) return 0;
   const MaskPlan mp = plan_mask(attn_mask, mask_kind, mask_strides, B, Hq, Sq, Skv);
   if (mp.route == kRouteCopied) return mp.copy_bytes;
   return mp.route == kRouteVt ? spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D) : 0;
@@ -1191,10 +1318,18 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     // Without a mask, short query runs pack q heads of a KV head into one
     // block's rows, so they share each K / V tile (decode: one block per
     // (sequence, KV head) instead of g mostly idle ones).
-    f2.pack = mask_kind == kNoMask ? pack_heads(B, Hkv, fa.g, Sq) : 1;
+    // And (plan_grid) a key split when the blocks would not fill the device
+    // and the workspace holds its partials.
+    GridPlan gpl;
+    if (mask_kind == kNoMask)
+      gpl = plan_grid(B, Hq, Hkv, Sq, Skv, D, is_causal != 0, workspace && aligned16(workspace) ? workspace_bytes : 0);
+    f2.pack = gpl.pack;
     f2.gp = fa.g / f2.pack;
     f2.qblocks = static_cast<int>((static_cast<int64_t>(f2.pack) * Sq + kQB - 1) / kQB);
-    const int64_t items = static_cast<int64_t>(B) * Hkv * f2.gp * f2.qblocks;
+    f2.nsplit = gpl.nsplit;
+    f2.split_keys = gpl.nsplit > 1 ? gpl.split_keys : Skv;
+    f2.part = gpl.nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
+    const int64_t items = blocks_for(B, Hkv, fa.g, Sq, f2.pack) * f2.nsplit;
     SPYRE_REQUIRE(items < (int64_t{1} << 31), SPYRE_EUNSUPPORTED, "too many query blocks");
     f2.n_items = static_cast<uint32_t>(items);
     f2.xcd_remap = items % 8 == 0;
@@ -1214,6 +1349,14 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
       launch_lds<kNoMask, 4>(f2, D, prescaled, st);  // blocks with fewer rows than wavefronts can fill
     else
       launch_lds<kNoMask>(f2, D, prescaled, st);
+    if (f2.nsplit > 1) {
+      const hipError_t e0 = hipGetLastError();
+      SPYRE_REQUIRE(e0 == hipSuccess, SPYRE_EHIP, "sdpa launch failed: %s", hipGetErrorString(e0));
+      MergeArgs ma{f2.part, f2.out, f2.lse, Hq, Sq, D, f2.nsplit, static_cast<int64_t>(B) * Hq * Sq};
+      const int64_t mblocks = (ma.rows * (D / 4) + 255) / 256;
+      SPYRE_REQUIRE(mblocks < (int64_t{1} << 31), SPYRE_EUNSUPPORTED, "too many rows");
+      sdpa_split_merge_kernel<<<dim3(static_cast<unsigned>(mblocks)), 256, 0, st>>>(ma);
+    }
   } else {
     const dim3 grid((Sq + kWaves * kQ - 1) / (kWaves * kQ), Hq, B);
     auto launch = [&](auto mk) {

@@ -92,16 +92,17 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
     s = 1.0 / math.sqrt(D) if scale is None else float(scale)
     out = torch.empty((B, Sq, Hq, D), dtype=torch.float16, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
-    # The call's workspace: none for masks the kernel stages as they lie, a
-    # copy with 16-byte rows for other fp16 / bool masks, V's relayout for
-    # fp32 masks.
+    # The call's workspace: without a mask, a key split's partials when the
+    # blocks would not fill the device (none for causal calls); none for
+    # masks the kernel stages as they lie, a copy with 16-byte rows for other
+    # fp16 / bool masks, V's relayout for fp32 masks.
     need = 0
-    if kind != MASK_NONE:
-        need = int(_lib.lib().spyre_sdpa_fwd_call_workspace_bytes(mask.data_ptr(), kind, mstrides, B, Hq, Hkv,
-                                                                  Sq, Skv, D))
+    if kind != MASK_NONE or not is_causal:
+        need = int(_lib.lib().spyre_sdpa_fwd_call_workspace_bytes(
+            mask.data_ptr() if mask is not None else None, kind, mstrides, B, Hq, Hkv, Sq, Skv, D))
     if workspace is None and need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
-    elif workspace is not None and need:
+    elif workspace is not None and need and kind != MASK_NONE:
         # a workspace that holds V's relayout also serves (the fp32-mask kernel runs)
         floor = min(need, workspace_bytes(B, Hkv, Skv, D))
         if workspace.numel() * workspace.element_size() < floor:
