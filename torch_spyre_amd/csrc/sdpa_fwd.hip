@@ -53,6 +53,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 using spyre_hip::u32x4_t;
 
 constexpr int kWaves = 4;
@@ -928,17 +929,28 @@ __global__ __launch_bounds__(256) void sdpa_split_merge_kernel(MergeArgs a) {
   const int64_t r = u / d4;
   const int d = static_cast<int>(u - r * d4) * 4;
   const float* pml = a.part + a.rows * a.nsplit * a.D + 2 * r * a.nsplit;
-  float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s)
-    if (pml[2 * s + 1] > 0.f) M = fmaxf(M, pml[2 * s]);
-  float L = 0.f;
+  const float* po = a.part + r * a.nsplit * a.D + d;
+  // One pass with a running max, 8 splits' partials loaded at a time.
+  float M = -INFINITY, L = 0.f;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < a.nsplit; ++s) {
-    const float ls = pml[2 * s + 1];
-    if (!(ls > 0.f)) continue;
-    const float w = exp2f(pml[2 * s] - M);
-    L += ls * w;
-    acc += *reinterpret_cast<const f32x4*>(a.part + (r * a.nsplit + s) * a.D + d) * w;
+  for (int s0 = 0; s0 < a.nsplit; s0 += 8) {
+    f32x2 ml[8];
+    f32x4 ov[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = s0 + j < a.nsplit;
+      ml[j] = in ? *reinterpret_cast<const f32x2*>(pml + 2 * (s0 + j)) : f32x2{-INFINITY, 0.f};
+      ov[j] = in ? *reinterpret_cast<const f32x4*>(po + (s0 + j) * a.D) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (!(ml[j][1] > 0.f)) continue;
+      const float Mn = fmaxf(M, ml[j][0]);
+      const float c = exp2f(M - Mn), w = exp2f(ml[j][0] - Mn);  // M = -inf: c = 0
+      L = L * c + ml[j][1] * w;
+      acc = acc * c + ov[j] * w;
+      M = Mn;
+    }
   }
   const int64_t qi = r % a.Sq, bh = r / a.Sq;
   const int64_t h = bh % a.Hq, b = bh / a.Hq;
