@@ -13,8 +13,8 @@ serve a step from the previous one.
 
 Also timed: under "more_configs", the dense MHA decode call (q [1, 8, 1, 64], k/v
 [1, 8, 512, 64]; absolute µs, launch-bound), the Llama-3-8B decode step through SDPA
-with dense K/V (q [32, 32, 1, 128], k/v [32, 8, 4096, 128]) and its long-context
-counterpart (q [4, 64, 1, 128], k/v [4, 8, 32768, 128]), the ragged batch (64 sequences, context
+with dense K/V (q [32, 32, 1, 128], k/v [32, 8, 4096, 128]), its batch-1 (absolute µs)
+and long-context (q [4, 64, 1, 128], k/v [4, 8, 32768, 128]) counterparts, the ragged batch (64 sequences, context
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
 heads, append one token at position 131072, attend over 131073 tokens) and
 prefill SDPA, causal, full and with an fp16 / boolean [4096, 4096] mask
@@ -178,6 +178,14 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
         "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
         "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb, "kernels_per_step": 1}
     del q2, k2, v2
+    # batch-1 decode through SDPA with dense K/V: q [1, 32, 1, 128], k/v
+    # [1, 8, 4096, 128] (keys split across blocks, partials merged)
+    q4 = torch.randn((1, HQ, 1, D), generator=gg, device=dev).half()
+    k4 = torch.randn((1, HKV, 4096, D), generator=gg, device=dev).half()
+    v4 = torch.randn((1, HKV, 4096, D), generator=gg, device=dev).half()
+    ms = timed(lambda i: tsa.scaled_dot_product_attention(q4, k4, v4, enable_gqa=True), steps, warmup, stream)
+    res["dense_gqa_decode_b1_h32_8_s4096"] = {"us_per_call": round(ms * 1e3, 2), "kernels_per_step": 2}
+    del q4, k4, v4
     # long-context decode through SDPA with dense K/V: q [4, 64, 1, 128],
     # k/v [4, 8, 32768, 128] (keys split across blocks, partials merged)
     q3 = torch.randn((4, 64, 1, D), generator=gg, device=dev).half()
