@@ -439,9 +439,13 @@ template <> struct MaskTile<kMaskBool> {  // 64 + 16 bytes per row
 // ahead, a barrier per step.  Four (calls without a mask whose blocks have
 // fewer than 256 rows, e.g. decode, where one wavefront computes and the
 // step waits on its loads): loads two steps ahead, a barrier per two steps.
-template <int D, bool PRESCALED, int MK, int SLOTS = 2>
+// HALF (blocks of at most 128 rows without a mask, e.g. decode): wavefronts
+// 2r and 2r + 1 share row tile r and take one 32-key half of every step
+// each; the pair's partials are folded in LDS at the end.
+template <int D, bool PRESCALED, int MK, int SLOTS = 2, bool HALF = false>
 __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   static_assert(SLOTS == 2 || (SLOTS == 4 && MK == kNoMask), "four slots leave no room for a mask");
+  static_assert(!HALF || MK == kNoMask, "half steps serve calls without a mask");
   using L = Lds2<D>;
   using MT = MaskTile<MK>;
   constexpr int DK = D / 16;  // QK k-steps
@@ -467,7 +471,8 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   const int b = static_cast<int>(r / a.Hkv);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   __builtin_assume(wave >= 0 && wave < kWaves2);  // lets the compiler drop always-true load guards
-  const int qw0 = qb * kQB, q0 = qw0 + wave * kQW;  // rows
+  const int hw = HALF ? (wave & 1) : 0;  // HALF: the key half of each step
+  const int qw0 = qb * kQB, q0 = qw0 + (HALF ? (wave >> 1) : wave) * kQW;  // rows
   const int col = lane & 31, half = lane >> 5;
   const int qrow = q0 + col;
   const int qi = pack == 1 ? qrow : qrow / pack;  // this lane's query
@@ -746,6 +751,99 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     }
   };
 
+  // HALF: the wavefront's S tile (keys 32 hw .. 32 hw + 31 of the step)
+  // lives in slot 0 of cur / nxt; its fragments are K half hw (vi < DK) and
+  // the V^T operands of keys 32 hw .. + 31 (vi - DK = j DM + dm).
+  constexpr int kNFH = DK + 2 * DM;
+  auto frag_h = [&](const _Float16* k1, int vi) -> f16x8 {
+    if (vi < DK)
+      return *reinterpret_cast<const f16x8*>(k1 + (hw * 32 + key32_of(col)) * L::kRowK + 8 * half + 16 * vi);
+    const int i = vi - DK;
+    const uint32_t e = vtr + (16 * (2 * hw + i / DM)) * L::kRowV + 32 * (i % DM);
+    const v4i16 lo = tr4(e), hi = tr4(e + 4 * L::kRowV);
+    return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  auto interleave_h = [](int i0, int i1) {
+    for (int i = i0; i < i1; ++i) {
+      const int f = i + kPrefetch;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (f < DK)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      else if (f < kNFH)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+  auto step_h = [&](int t, f32x16& cur, f32x16& nxt) {
+    const _Float16* k1 = lds + ((t + 1) % SLOTS) * L::kSlot;
+    if constexpr (SLOTS == 2) {
+      if (t + 2 < n_tiles) dma_k(kb0 + (t + 2) * kKT, t & 1);
+      if (t + 1 < n_tiles) dma_v(kb0 + (t + 1) * kKT, (t + 1) & 1);
+    } else if ((t & 1) == 0) {
+      if (t + 3 < n_tiles) dma_k(kb0 + (t + 3) * kKT, (t + 3) % 4);
+      if (t + 4 < n_tiles) dma_k(kb0 + (t + 4) * kKT, t % 4);
+      if (t + 2 < n_tiles) dma_v(kb0 + (t + 2) * kKT, (t + 2) % 4);
+      if (t + 3 < n_tiles) dma_v(kb0 + (t + 3) * kKT, (t + 3) % 4);
+    }
+    if (active(t)) {
+      vtr = static_cast<uint32_t>((t % SLOTS) * L::kSlot + L::kK) + vtr_lane;
+      asm volatile("" : "+v"(vtr));
+      f16x8 fr[kNFH];
+#pragma unroll
+      for (int i = 0; i < kPrefetch; ++i) fr[i] = frag_h(k1, i);
+      auto mfma = [&](int i, const f16x8& b, f32x16& acc) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[i], b, acc, 0, 0, 0);
+        if (i + kPrefetch < kNFH) fr[i + kPrefetch] = frag_h(k1, i + kPrefetch);
+      };
+      if (edge(t)) {  // the key test on this half
+        const int kl = key_last - (kb0 + t * kKT) - 32 * hw - 8 * half;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr)
+          cur[rr] = key32_of(8 * (rr >> 2) + (rr & 3)) <= kl ? cur[rr] : -INFINITY;
+      }
+      nxt = PRESCALED ? neg_m_tile : f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < DK; ++ks) mfma(ks, qv[ks], nxt);
+      interleave_h(0, DK);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, cur[rr]);
+      mx = PRESCALED ? max_xor32(mx) + m_use : max_xor32(mx) * scale_abs;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + 8.f) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+        m_run = m_new;
+        if constexpr (PRESCALED) {
+          const float m_use_new = m_new == -INFINITY ? m_use : m_new;
+          const float d = m_use_new - m_use;
+          m_use = m_use_new;
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            cur[rr] -= d;
+            nxt[rr] -= d;
+            neg_m_tile[rr] = -m_use;
+          }
+        }
+      }
+      const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+      f16x8 p[2];
+      softmax_half(cur, neg_m, p);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int dm = 0; dm < DM; ++dm) mfma(DK + j * DM + dm, p[j], o[dm]);
+      interleave_h(DK, kNFH);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (SLOTS == 2 || (t & 1)) {
+      dma_wait();
+      __syncthreads();
+    }
+  };
+
   // Step t: LDS holds K(t+1) in slot (t+1)&1 and V(t) in slot t&1, cur
   // holds S(t); the step loads K(t+2) and V(t+1) and leaves S(t+1) in nxt.
   // The MFMAs of S(t+1) and of step t's P V overlap step t's softmax: each
@@ -866,14 +964,51 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   dma_wait();
   __syncthreads();
   if (active(0)) {
-    sa[0] = qk(lds, 0);
-    sa[1] = qk(lds, 1);
+    if constexpr (HALF) {
+      sa[0] = qk(lds, hw);
+    } else {
+      sa[0] = qk(lds, 0);
+      sa[1] = qk(lds, 1);
+    }
   }
   __syncthreads();  // step 0 overwrites K(0)
   // Two steps per iteration, S(t) alternating between sa and sb.
   for (int t = 0; t < n_tiles; t += 2) {
-    step(t, sa, sb);
-    if (t + 1 < n_tiles) step(t + 1, sb, sa);
+    if constexpr (HALF) {
+      step_h(t, sa[0], sb[0]);
+      if (t + 1 < n_tiles) step_h(t + 1, sb[0], sa[0]);
+    } else {
+      step(t, sa, sb);
+      if (t + 1 < n_tiles) step(t + 1, sb, sa);
+    }
+  }
+  if constexpr (HALF) {
+    // Fold each pair: wavefront 2r + 1 leaves O, m, l (per lane) in LDS,
+    // 2r weights both by exp2(m - max) (a half that saw no key weighs 0).
+    dma_wait();
+    __syncthreads();  // every wavefront is done with the tiles
+    constexpr int kRec = DM * 16 + 2;
+    float* rec = reinterpret_cast<float*>(lds) + ((wave >> 1) * 64 + lane) * kRec;
+    if (hw == 1) {
+#pragma unroll
+      for (int dm = 0; dm < DM; ++dm)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) rec[dm * 16 + k] = o[dm][k];
+      rec[DM * 16] = m_run;
+      rec[DM * 16 + 1] = l_run;
+    }
+    __syncthreads();
+    if (hw == 1) return;
+    const float m1 = rec[DM * 16], l1 = rec[DM * 16 + 1];
+    const float M = fmaxf(m_run, m1);
+    const float w0 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - M);
+    const float w1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - M);
+#pragma unroll
+    for (int dm = 0; dm < DM; ++dm)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) o[dm][k] = o[dm][k] * w0 + rec[dm * 16 + k] * w1;
+    l_run = l_run * w0 + l1 * w1;
+    m_run = M;
   }
 
   const float l = sum_xor32(l_run);
@@ -1020,17 +1155,17 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
   return gp;
 }
 
-template <int MK, int SLOTS = 2>
+template <int MK, int SLOTS = 2, bool HALF = false>
 void launch_lds(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
   const dim3 grid(f2.n_items);
   if (D == 128 && prescaled)
-    sdpa_fwd_lds_kernel<128, true, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<128, true, MK, SLOTS, HALF><<<grid, kThreads2, 0, st>>>(f2);
   else if (D == 128)
-    sdpa_fwd_lds_kernel<128, false, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<128, false, MK, SLOTS, HALF><<<grid, kThreads2, 0, st>>>(f2);
   else if (prescaled)
-    sdpa_fwd_lds_kernel<64, true, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<64, true, MK, SLOTS, HALF><<<grid, kThreads2, 0, st>>>(f2);
   else
-    sdpa_fwd_lds_kernel<64, false, MK, SLOTS><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_fwd_lds_kernel<64, false, MK, SLOTS, HALF><<<grid, kThreads2, 0, st>>>(f2);
 }
 
 // A copy of a mask with 16-byte rows: [bm][hm][qm][pitch bytes], keys past
@@ -1357,6 +1492,8 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
       launch_lds<kMaskF16>(f2, D, prescaled, st);
     else if (mask_kind == kMaskBool)
       launch_lds<kMaskBool>(f2, D, prescaled, st);
+    else if (static_cast<int64_t>(f2.pack) * Sq <= kQB / 2)
+      launch_lds<kNoMask, 4, true>(f2, D, prescaled, st);  // half steps: two wavefronts per row tile
     else if (static_cast<int64_t>(f2.pack) * Sq < kQB)
       launch_lds<kNoMask, 4>(f2, D, prescaled, st);  // blocks with fewer rows than wavefronts can fill
     else
