@@ -118,6 +118,55 @@ def test_gqa_heads_packed_into_rows(cuda, Sq, Skv, causal):
     assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
 
 
+@pytest.mark.parametrize("B,Hq,Sq,Skv,causal", [(16, 64, 1, 512, False), (16, 64, 1, 512, True),
+                                                (8, 64, 4, 300, False), (8, 64, 4, 300, True)])
+def test_gqa_heads_partly_packed(cuda, B, Hq, Sq, Skv, causal):
+    """Grids where only some of a KV head's 8 q heads share a block (on a
+    256-CU device: 4 per block at B 16 / Sq 1, 2 per block at B 8 / Sq 4):
+    every q head must be computed, each by the block holding its group."""
+    q = randn((B, Hq, Sq, 128), SEED + 60 + B)
+    k, v = randn((B, 8, Skv, 128), SEED + 61), randn((B, 8, Skv, 128), SEED + 62)
+    out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, is_causal=causal))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, is_causal=causal, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
+def test_key_split_many_runs(cuda):
+    """Decode over 16484 keys with 1 sequence and 8 KV heads: the key split
+    runs 29 blocks per row (more than the merge pass loads at a time, the
+    last group ragged); out against CPU fp32, LSE against fp64."""
+    q = randn((1, 32, 1, 128), SEED + 70)
+    k, v = randn((1, 8, 16484, 128), SEED + 71), randn((1, 8, 16484, 128), SEED + 72)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
+    err = np.abs(lse.cpu().numpy() - lse64).max()
+    assert err <= LSE_ATOL, err
+    # every key counted once: q = 0 makes every score 0, so LSE = ln(Skv)
+    # exactly up to fp32 rounding (a lost 356-key split moves it by 0.022,
+    # one lost key by 6e-5)
+    out0, lse0 = run(cuda, torch.zeros_like(q), k, v, enable_gqa=True, return_lse=True)
+    assert np.abs(lse0.cpu().numpy() - math.log(16484)).max() <= 4e-6
+    assert_close(out0, v.float().mean(dim=2, keepdim=True).repeat_interleave(4, dim=1))
+
+
+def test_operand_views_copied(cuda):
+    """Operands torch counts as contiguous but the kernel cannot read as they
+    lie (an odd stride on a size-1 dim; a storage offset that is not 16-byte
+    aligned) are copied, not refused."""
+    q = randn((2, 4, 1, 64), SEED + 80)
+    k, v = randn((2, 4, 40, 64), SEED + 81), randn((2, 4, 40, 64), SEED + 82)
+    q_odd = torch.as_strided(q.to(cuda), (2, 4, 1, 64), (256, 64, 3, 1))
+    assert q_odd.is_contiguous()
+    flat = torch.empty(k.numel() + 1, dtype=torch.float16, device=cuda)
+    k_off = flat[1:].view(k.shape)
+    k_off.copy_(k.to(cuda))
+    assert k_off.is_contiguous() and k_off.data_ptr() % 16 != 0
+    out = run(cuda, q_odd, k_off, v)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
+
+
 @pytest.mark.parametrize("kind", ["f16", "f32", "bool"])
 @pytest.mark.parametrize("shape", ["qk", "b1qk", "1h1k"])
 def test_masks_broadcast(cuda, kind, shape):

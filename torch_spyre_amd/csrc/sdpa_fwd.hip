@@ -453,7 +453,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // Two K / V slots, then (masked calls) two mask blocks per wavefront.
   __shared__ __align__(16) _Float16 lds[SLOTS * L::kSlot + kWaves2 * MT::kBytes];
 
-  // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * g + gi: the
+  // item = ((b * Hkv + kvh) * qblocks + (qblocks - 1 - qb)) * gp + gi: the
   // blocks of one (sequence, KV head) are consecutive, latest query block
   // (longest, under causal masking) first across its g q heads.
   // With pack > 1 a block's rows are (query, q head) pairs of one KV head,
@@ -476,7 +476,8 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   const int col = lane & 31, half = lane >> 5;
   const int qrow = q0 + col;
   const int qi = pack == 1 ? qrow : qrow / pack;  // this lane's query
-  const int h = kvh * a.g + (pack == 1 ? gi : qrow - qi * pack);
+  // Block gi of the KV head holds q heads gi * pack .. gi * pack + pack - 1.
+  const int h = kvh * a.g + gi * pack + (qrow - qi * pack);
   const bool q_ok = qi < a.Sq;
   // The wavefront's first and last query, and the block's last.
   const int q_lo = pack == 1 ? q0 : q0 / pack;

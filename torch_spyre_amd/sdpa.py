@@ -54,7 +54,9 @@ def _operand(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype != torch.float16:
         raise TypeError(f"{name} must be float16 (got {t.dtype})")
     ok = t.stride(3) == 1 and all(t.stride(i) % 8 == 0 for i in range(3)) and t.data_ptr() % 16 == 0
-    return t if ok else t.contiguous()
+    # contiguous() would hand back a tensor torch already counts as
+    # contiguous (odd strides on size-1 dims, an unaligned storage offset)
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
 def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
