@@ -191,6 +191,29 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
                                       int Hkv, int D, int max_context_len, int split_tokens,
                                       void* stream);
 
+/* Bytes of the chunk-partial scratch that spyre_paged_decode_attn_noalloc_f16
+ * keeps in the library (one copy per GPU, held until the process ends). */
+#define SPYRE_DECODE_SCRATCH_BYTES (16u << 20)
+
+/* spyre_paged_decode_attn_f16 without a workspace argument: the chunk
+ * partials go to a scratch array the library holds on each GPU, so the call
+ * allocates nothing (no hipMalloc / hipFree, no library allocation).
+ * Same arguments (less the workspace), kernels and results as
+ * spyre_paged_decode_attn_f16.  Returns SPYRE_ENOSPC, before any HIP call,
+ * when spyre_paged_decode_attn_workspace_bytes of the call exceeds
+ * SPYRE_DECODE_SCRATCH_BYTES (e.g. B 64, 32 / 8 heads, D 128, contexts up
+ * to 32768 tokens need 8.1 MiB).  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (two streams, two threads) race.
+ * No counterpart in the reference: it serves callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * allocation). */
+int spyre_paged_decode_attn_noalloc_f16(const void* q, const void* k_cache, const void* v_cache,
+                                        const int32_t* block_table, int64_t bt_stride,
+                                        const int32_t* context_lens, void* out, float* lse, int B,
+                                        int Hq, int Hkv, int D, int page_size, int64_t num_pages,
+                                        int max_context_len, int split_tokens, float scale,
+                                        void* stream);
+
 /* Attention mask kinds of spyre_sdpa_fwd_f16. */
 #define SPYRE_MASK_NONE 0
 #define SPYRE_MASK_F16 1  /* additive fp16 bias                */

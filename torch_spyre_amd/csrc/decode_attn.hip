@@ -44,6 +44,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <mutex>
 
 #include "spyre_common.h"
 
@@ -743,4 +744,70 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
   if (!p.multi_chunk) return SPYRE_OK;  // pass 1 wrote every output
   p.ma.skip_single = 1;
   return launch_merge(p, st);
+}
+
+// ------------------------------------------ the entry that allocates nothing --
+
+// The chunk partials of spyre_paged_decode_attn_noalloc_f16.  Each GPU holds
+// its own copy from the library's load to the end of the process.  In host
+// code this name is a stand-in, not a device address: kernel arguments use
+// the address scratch_address() returns for the current device.
+static __device__ __align__(256) unsigned char scratch[SPYRE_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The current device's address of `scratch`, taken once per device (with
+// that device current) by hipGetSymbolAddress; nullptr, with the error
+// recorded, when the runtime cannot give it.
+void* scratch_address() {
+  static std::atomic<void*> addr[kMaxDevices];
+  static std::mutex mu;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    spyre_hip::set_error("no usable current device (%s, device %d)", hipGetErrorString(e), dev);
+    return nullptr;
+  }
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(mu);
+  p = addr[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      spyre_hip::set_error("hipGetSymbolAddress of the decode scratch failed on device %d: %s", dev,
+                           hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+}  // namespace
+
+extern "C" int spyre_paged_decode_attn_noalloc_f16(const void* q, const void* k_cache,
+                                                   const void* v_cache, const int32_t* block_table,
+                                                   int64_t bt_stride, const int32_t* context_lens,
+                                                   void* out, float* lse, int B, int Hq, int Hkv,
+                                                   int D, int page_size, int64_t num_pages,
+                                                   int max_context_len, int split_tokens,
+                                                   float scale, void* stream) {
+  spyre_hip::clear_error();
+  // Checked before any HIP call: a call that does not fit never touches the device.
+  const size_t need =
+      spyre_paged_decode_attn_workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens);
+  SPYRE_REQUIRE(need <= SPYRE_DECODE_SCRATCH_BYTES, SPYRE_ENOSPC,
+                "decode needs %zu bytes of chunk partials, more than the %zu bytes of the "
+                "library's scratch; pass a workspace to spyre_paged_decode_attn_f16 instead",
+                need, static_cast<size_t>(SPYRE_DECODE_SCRATCH_BYTES));
+  void* ws = scratch_address();
+  if (!ws) return SPYRE_EHIP;
+  // Nothing in the scratch needs clearing: the split pass writes every
+  // partial the merge pass uses, and the merge discards the rest by selects.
+  return spyre_paged_decode_attn_f16(q, k_cache, v_cache, block_table, bt_stride, context_lens, out,
+                                     lse, ws, SPYRE_DECODE_SCRATCH_BYTES, B, Hq, Hkv, D, page_size,
+                                     num_pages, max_context_len, split_tokens, scale, stream);
 }
