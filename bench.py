@@ -353,7 +353,7 @@ def main():
     xs = [bits16(i) for i in range(nbuf)]
     dflt = tsa.SpyreTensorLayout([R, C], torch.float16)
     trl = tsa.transpose_restick_layout(R, C)
-    devs = [tsa.to_device_layout(x, dflt) for x in xs]
+    devs = [tsa.device_buffer(tsa.to_device_layout(x, dflt)) for x in xs]
     outs_dev = [torch.empty_like(d) for d in devs]
     outs_host = [torch.empty_like(x) for x in xs]
     to_plan = tsa.dma_plan([R, C], [C, 1], [C, 1], 0, dflt, True)

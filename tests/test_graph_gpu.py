@@ -78,8 +78,8 @@ def test_relayout_graph_replays_match_oracle(cuda):
     x = torch.empty((R, C), dtype=torch.float16, device=cuda)
     stl = tsa.SpyreTensorLayout([R, C], torch.float16)
     trl = tsa.transpose_restick_layout(R, C)
-    dev = tsa.spyre_empty_with_layout([R, C], [C, 1], torch.float16, stl, cuda)
-    tr = tsa.spyre_empty_with_layout([R, C], [C, 1], torch.float16, trl, cuda)
+    dev = tsa.device_buffer(tsa.spyre_empty_with_layout([R, C], [C, 1], torch.float16, stl, cuda))
+    tr = tsa.device_buffer(tsa.spyre_empty_with_layout([R, C], [C, 1], torch.float16, trl, cuda))
     to_sticks = tsa.DmaCopy(x, dev, tsa.dma_plan([R, C], [C, 1], [C, 1], 0, stl, True))
     restick = tsa.DmaCopy(dev, tr, [tsa.restick_plan([R, C], stl, trl)])
 

@@ -41,5 +41,5 @@ def test_planned_restickifies_run_on_gpu(cuda, name):
         o = OL.stl_init(size, strides, "float16", _order(entry["target_layout"]))
         assert (list(dst.device_size), list(dst.stride_map)) == (o.device_size, o.stride_map)
         want = OL.h2d(bits, size, strides, 0, o)
-        got = out.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        got = tsa.device_buffer(out).contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
         assert np.array_equal(got[: want.size], want), (name, op, buf)

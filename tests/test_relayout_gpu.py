@@ -27,6 +27,11 @@ def _bits_tensor(bits: np.ndarray, device) -> torch.Tensor:
 
 
 def _as_bits(t: torch.Tensor) -> np.ndarray:
+    """Raw 16-bit patterns; a SpyreTensor gives its buffer in stick order."""
+    import torch_spyre_amd as tsa
+
+    if isinstance(t, tsa.SpyreTensor):
+        t = tsa.device_buffer(t)
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
@@ -71,7 +76,7 @@ def test_config2_transpose_restick_full(cuda):
     assert np.array_equal(_as_bits(out), want)
     assert np.array_equal(_as_bits(out2), want)
     # and back
-    back = tsa.from_device_layout(out, dst, [4096, 4096])
+    back = tsa.from_device_layout(out)
     assert np.array_equal(_as_bits(back), bits)
 
 
@@ -156,7 +161,7 @@ def test_prepared_dma_copy_matches(cuda):
     bits = OR.random_finite_f16_bits(tuple(sizes), SEED + 17)
     x = _bits_tensor(bits, cuda)
     stl = tsa.SpyreTensorLayout(sizes, torch.float16)
-    want = tsa.to_device_layout(x, stl)
+    want = tsa.device_buffer(tsa.to_device_layout(x, stl))
     out = torch.zeros_like(want)
     call = tsa.DmaCopy(x, out, tsa.dma_plan(sizes, [2112, 1], [2112, 1], 0, stl, True))
     for _ in range(3):
@@ -295,5 +300,5 @@ def test_empty_and_errors(cuda):
     info.rank, info.size[0], info.stride_src[0], info.stride_dst[0] = 1, 128, 1, 1
     with pytest.raises(SpyreHipError):
         tsa.relayout.dma_copy(src, dst, [info])
-    with pytest.raises(RuntimeError):
-        tsa.to_device_layout(torch.zeros(64, 64, dtype=torch.float16), stl)  # CPU tensor: no CPU path
+    with pytest.raises(RuntimeError):  # CPU buffers: no CPU path
+        tsa.relayout.h2d_buffer(torch.zeros(64, 64, dtype=torch.float16), stl)

@@ -23,14 +23,20 @@ from .layout import (  # noqa: E402
 )
 from .relayout import (  # noqa: E402
     DmaCopy,
+    overwrite,
+    transpose_restick_layout,
+)
+from .device_tensor import (  # noqa: E402
+    SpyreTensor,
     copy_tensor,
+    device_buffer,
     device_tensor_layout,
     from_device_layout,
-    overwrite,
     restickify,
+    restickify_target_layout,
+    set_restickify_target,
     spyre_empty_with_layout,
     to_device_layout,
-    transpose_restick_layout,
 )
 from .attention import (  # noqa: E402
     PagedDecode,
@@ -48,16 +54,18 @@ from .attention import (  # noqa: E402
 from .sdpa import (  # noqa: E402
     Unsupported,
     scaled_dot_product_attention,
+    sdpa_override,
     sdpa_overrideable,
 )
 from . import ops  # noqa: E402,F401  (registers the spyre:: ops)
 
 __all__ = [
     "DataFormats", "ElementArrangement", "SpyreTensorLayout", "dma_plan", "get_device_dtype",
-    "restick_plan", "DmaCopy", "copy_tensor", "device_tensor_layout", "from_device_layout", "overwrite",
-    "restickify", "spyre_empty_with_layout", "to_device_layout", "transpose_restick_layout",
+    "restick_plan", "DmaCopy", "overwrite", "transpose_restick_layout",
+    "SpyreTensor", "copy_tensor", "device_buffer", "device_tensor_layout", "from_device_layout", "restickify",
+    "restickify_target_layout", "set_restickify_target", "spyre_empty_with_layout", "to_device_layout",
     "PagedDecode", "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
     "paged_decode_merge", "paged_decode_split",
     "sdpa_decode", "v_page_layout", "workspace_bytes",
-    "Unsupported", "scaled_dot_product_attention", "sdpa_overrideable",
+    "Unsupported", "scaled_dot_product_attention", "sdpa_override", "sdpa_overrideable",
 ]

@@ -25,7 +25,7 @@ import torch
 
 from . import _lib
 from .layout import DataFormats, SpyreTensorLayout
-from .relayout import _require_cuda, _stream_ptr, to_device_layout
+from .relayout import _require_cuda, _stream_ptr, h2d_buffer
 
 PAGE = 64
 # Wavefronts per decode workgroup: a sequence is cut into chunks of at most
@@ -76,8 +76,8 @@ class PagedKVCache:
         self.num_pages, self.Hkv, self.D = P, Hkv, D
         self.k_layout = k_page_layout(P, Hkv, D)
         self.v_layout = v_page_layout(P, Hkv, D)
-        self.k = to_device_layout(k_pages, self.k_layout).view(P, Hkv, D // 64, PAGE, 64)
-        self.v = to_device_layout(v_pages, self.v_layout).view(P, Hkv, D, PAGE)
+        self.k = h2d_buffer(k_pages, self.k_layout).view(P, Hkv, D // 64, PAGE, 64)
+        self.v = h2d_buffer(v_pages, self.v_layout).view(P, Hkv, D, PAGE)
         return self
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, block_table: torch.Tensor,
@@ -305,8 +305,8 @@ def dense_to_pages(k: torch.Tensor, v: torch.Tensor) -> tuple[PagedKVCache, torc
     cache.num_pages, cache.Hkv, cache.D = B * P, Hkv, D
     cache.k_layout = k_page_layout(B * P, Hkv, D)
     cache.v_layout = v_page_layout(B * P, Hkv, D)
-    cache.k = to_device_layout(k5, k_lay).view(B * P, Hkv, D // 64, PAGE, 64)
-    cache.v = to_device_layout(v5, v_lay).view(B * P, Hkv, D, PAGE)
+    cache.k = h2d_buffer(k5, k_lay).view(B * P, Hkv, D // 64, PAGE, 64)
+    cache.v = h2d_buffer(v5, v_lay).view(B * P, Hkv, D, PAGE)
     table = torch.arange(B * P, dtype=torch.int32, device=k.device).view(B, P)
     return cache, table
 

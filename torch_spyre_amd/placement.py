@@ -31,7 +31,7 @@ some dim of the buffer carries ``v`` (a restickify moves the stick there);
 otherwise infinite ("no mechanism to gather / scatter", optimize_restickify.py:227-238).
 
 Host logic only; the restickifies a plan lists run on the GPU through
-``relayout.restickify`` (``schedule`` gives each as a source and target
+``restickify`` (``schedule`` gives each as a source and target
 SpyreTensorLayout).
 """
 

@@ -7,10 +7,9 @@ storage is in the stick layout.  The reference's DMA descriptors
 (torch_spyre/csrc/spyre_mem.cpp:176-440) are computed by the native library
 and executed by its HIP kernels (spyre_dma_copy).
 
-A device tensor returned here has shape ``layout.device_size`` (contiguous)
-and carries its layout and host geometry as attributes, read back with
-``device_tensor_layout`` (the reference's Tensor.device_tensor_layout,
-torch_spyre/_monkey_patch.py:63-71).
+This module works on plain buffers: a buffer in stick order holds a host
+geometry (sizes, strides) in a SpyreTensorLayout.  device_tensor.py builds
+the Spyre tensor (logical geometry, views, copies) on top of it.
 """
 
 from __future__ import annotations
@@ -79,36 +78,26 @@ class DmaCopy:
         _lib.check("spyre_dma_copy", self._fn(*self._args, _stream_ptr(self._device)))
 
 
-def _tag(t: torch.Tensor, layout: SpyreTensorLayout, size, stride) -> torch.Tensor:
-    t._spyre_layout = layout
-    t._spyre_host_size = [int(v) for v in size]
-    t._spyre_host_stride = [int(v) for v in stride]
-    return t
-
-
-def device_tensor_layout(t: torch.Tensor) -> Optional[SpyreTensorLayout]:
-    """Layout of a device tensor made by this module, else None."""
-    return getattr(t, "_spyre_layout", None)
-
-
-def spyre_empty_with_layout(size: Sequence[int], stride: Sequence[int], dtype: torch.dtype,
-                            device_layout: SpyreTensorLayout, device=None, *,
-                            zero: bool = True) -> torch.Tensor:
-    """Allocates a device tensor for a host tensor of (size, stride) in
-    ``device_layout``: max(stick bytes, host bytes), as
-    torch_spyre/csrc/spyre_mem.cpp:547-579.  Zero-filled unless ``zero`` is
-    False (padding positions are never written by the relayout)."""
-    device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+def alloc_bytes(size: Sequence[int], dtype: torch.dtype, layout: SpyreTensorLayout) -> int:
+    """Allocation of a host tensor of ``size`` in ``layout``:
+    max(128 x prod(device_size[:-1]), host bytes)
+    (torch_spyre/csrc/spyre_mem.cpp:468-473, :547-579)."""
     esz = torch.empty((), dtype=dtype).element_size()
-    dev_bytes = device_layout.device_size_in_bytes()
-    host_bytes = math.prod(int(v) for v in size) * esz
-    ds = list(device_layout.device_size)
-    if math.prod(ds) * esz == dev_bytes and dev_bytes >= host_bytes:
-        shape = ds
-    else:
-        shape = [max(dev_bytes, host_bytes) // esz]
-    t = (torch.zeros if zero else torch.empty)(shape, dtype=dtype, device=device)
-    return _tag(t, device_layout, size, stride)
+    return max(layout.device_size_in_bytes(), math.prod(int(v) for v in size) * esz)
+
+
+def alloc_shape(size: Sequence[int], dtype: torch.dtype, layout: SpyreTensorLayout) -> list[int]:
+    """Shape of the buffer holding that allocation: ``device_size`` when the
+    allocation is exactly the layout's elements, else flat."""
+    esz = torch.empty((), dtype=dtype).element_size()
+    ds = list(layout.device_size)
+    nbytes = alloc_bytes(size, dtype, layout)
+    return ds if math.prod(ds) * esz == nbytes else [nbytes // esz]
+
+
+def alloc_buffer(size: Sequence[int], dtype: torch.dtype, layout: SpyreTensorLayout, device,
+                 zero: bool = True) -> torch.Tensor:
+    return (torch.zeros if zero else torch.empty)(alloc_shape(size, dtype, layout), dtype=dtype, device=device)
 
 
 def _check_layout_dtype(dtype: torch.dtype, layout: SpyreTensorLayout) -> None:
@@ -124,85 +113,98 @@ def _covers_all(infos, layout: SpyreTensorLayout) -> bool:
     return n >= math.prod(layout.device_size)
 
 
-def to_device_layout(x: torch.Tensor, device_layout: SpyreTensorLayout) -> torch.Tensor:
-    """x (any strides) -> new device tensor in ``device_layout``.
-
-    The reference's ``Tensor.to(device_layout=stl)`` + ``copy_tensor``
-    (torch_spyre/_monkey_patch.py:106-155, torch_spyre/csrc/spyre_mem.cpp:594-651):
-    the device tensor keeps x's sizes and strides as its dma geometry."""
+def h2d_into(x: torch.Tensor, buf: torch.Tensor, layout: SpyreTensorLayout,
+             dma_stride: Sequence[int]) -> None:
+    """Writes host-order x (any strides) into ``buf`` in ``layout``, whose
+    stride_map refers to a host geometry of x's sizes and ``dma_stride``."""
     _require_cuda(x, "x")
-    _check_layout_dtype(x.dtype, device_layout)
+    _require_cuda(buf, "buf")
+    _check_layout_dtype(x.dtype, layout)
+    if x.numel() == 0:
+        return
+    dma_copy(x, buf, dma_plan(list(x.size()), list(dma_stride), list(x.stride()), x.storage_offset(), layout, True))
+
+
+def h2d_buffer(x: torch.Tensor, layout: SpyreTensorLayout) -> torch.Tensor:
+    """A new buffer holding x (any strides) in ``layout``, whose stride_map
+    refers to x's own sizes and strides."""
+    _require_cuda(x, "x")
+    _check_layout_dtype(x.dtype, layout)
     size, stride = list(x.size()), list(x.stride())
-    if x.numel() == 0:  # nothing to move
-        return spyre_empty_with_layout(size, stride, x.dtype, device_layout, x.device)
-    infos = dma_plan(size, stride, stride, x.storage_offset(), device_layout, True)
-    dst = spyre_empty_with_layout(size, stride, x.dtype, device_layout, x.device,
-                                  zero=not _covers_all(infos, device_layout))
-    dma_copy(x, dst, infos)
-    return dst
+    if x.numel() == 0:
+        return alloc_buffer(size, x.dtype, layout, x.device)
+    infos = dma_plan(size, stride, stride, x.storage_offset(), layout, True)
+    buf = alloc_buffer(size, x.dtype, layout, x.device, zero=not _covers_all(infos, layout))
+    dma_copy(x, buf, infos)
+    return buf
 
 
-def from_device_layout(dev: torch.Tensor, device_layout: Optional[SpyreTensorLayout] = None,
-                       size: Optional[Sequence[int]] = None,
-                       stride: Optional[Sequence[int]] = None) -> torch.Tensor:
-    """Device tensor -> new strided tensor (the reference's ``.cpu()`` D2H,
-    torch_spyre/csrc/spyre_mem.cpp:594-651).  Geometry defaults to what
-    ``to_device_layout`` recorded; the result has those strides."""
-    _require_cuda(dev, "dev")
-    layout = device_layout or device_tensor_layout(dev)
-    if layout is None:
-        raise ValueError("dev carries no layout; pass device_layout")
-    size = list(size if size is not None else dev._spyre_host_size)
-    if stride is None:
-        stride = getattr(dev, "_spyre_host_stride", None) if size == getattr(dev, "_spyre_host_size", None) else None
-    stride = list(stride) if stride is not None else _contiguous_strides(size)
-    _check_layout_dtype(dev.dtype, layout)
-    out = torch.empty_strided(size, stride, dtype=dev.dtype, device=dev.device)
+def d2h_buffer(buf: torch.Tensor, layout: SpyreTensorLayout, size: Sequence[int],
+               stride: Sequence[int]) -> torch.Tensor:
+    """A new strided CUDA tensor of (size, stride) read from ``buf`` in
+    ``layout`` (the DMA geometry the buffer was written with)."""
+    _require_cuda(buf, "buf")
+    _check_layout_dtype(buf.dtype, layout)
+    size, stride = list(size), list(stride)
+    out = torch.empty_strided(size, stride, dtype=buf.dtype, device=buf.device)
     if out.numel() == 0:
         return out
-    dma_copy(dev, out, dma_plan(size, stride, stride, 0, layout, False))
+    dma_copy(buf, out, dma_plan(size, stride, stride, 0, layout, False))
     return out
 
 
-def copy_tensor(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
-    """The reference's _C.copy_tensor (torch_spyre/csrc/module.cpp:339-341):
-    H2D when dst carries a layout, D2H when src does."""
-    if device_tensor_layout(dst) is not None:
-        lay = device_tensor_layout(dst)
-        size, stride = list(src.size()), list(src.stride())
-        dma_copy(src, dst, dma_plan(size, dst._spyre_host_stride, stride, src.storage_offset(), lay, True))
-        return dst
-    if device_tensor_layout(src) is not None:
-        lay = device_tensor_layout(src)
-        dma_copy(src, dst, dma_plan(list(dst.size()), src._spyre_host_stride, list(dst.stride()),
-                                    dst.storage_offset(), lay, False))
-        return dst
-    raise ValueError("copy_tensor: neither tensor carries a device layout")
+def copy_buffer(src: torch.Tensor, dst: torch.Tensor) -> None:
+    """dst <- src byte for byte (same allocation size): one flat DMA nest."""
+    if src.untyped_storage().nbytes() != dst.untyped_storage().nbytes() or src.dtype != dst.dtype:
+        raise ValueError("copy_buffer: allocations differ")
+    n = src.untyped_storage().nbytes() // src.element_size()
+    if n == 0:
+        return
+    info = _lib.StrideInfo()
+    info.rank = 1
+    info.size[0], info.stride_src[0], info.stride_dst[0] = n, 1, 1
+    dma_copy(src, dst, [info])
 
 
-def restickify(dev: torch.Tensor, dst_layout: SpyreTensorLayout,
-               src_layout: Optional[SpyreTensorLayout] = None,
-               host_size: Optional[Sequence[int]] = None) -> torch.Tensor:
-    """Device-to-device relayout of the same host tensor into ``dst_layout``
-    (the reference's spyre::restickify, whose target layout is computed by
-    torch_spyre/_inductor/pass_utils.py:749-833).  One pass when the two
-    tilings nest; otherwise through a host-order buffer (two passes)."""
-    _require_cuda(dev, "dev")
-    src_layout = src_layout or device_tensor_layout(dev)
-    if src_layout is None:
-        raise ValueError("dev carries no layout; pass src_layout")
-    size = list(host_size if host_size is not None else dev._spyre_host_size)
-    _check_layout_dtype(dev.dtype, dst_layout)
-    dense = getattr(dev, "_spyre_host_stride", _contiguous_strides(size)) == _contiguous_strides(size)
-    info = restick_plan(size, src_layout, dst_layout) if dense else None
-    if info is None:
-        host = from_device_layout(dev, src_layout, size, _contiguous_strides(size))
-        return to_device_layout(host, dst_layout)
-    exact = math.prod(info.size[: info.rank]) >= math.prod(dst_layout.device_size)
-    out = spyre_empty_with_layout(size, _contiguous_strides(size), dev.dtype, dst_layout, dev.device,
-                                  zero=not exact)
-    dma_copy(dev, out, [info])
-    return out
+def relayout_into(src: torch.Tensor, dst: torch.Tensor, host_size: Sequence[int], host_stride: Sequence[int],
+                  src_layout: SpyreTensorLayout, dst_layout: SpyreTensorLayout) -> None:
+    """dst (in dst_layout) <- src (in src_layout), both holding the host
+    geometry (host_size, host_stride).  One pass when the geometry is dense
+    and the two tilings nest (spyre_restick_plan); otherwise through host
+    order (two passes)."""
+    _require_cuda(src, "src")
+    _require_cuda(dst, "dst")
+    _check_layout_dtype(src.dtype, dst_layout)
+    size, stride = list(host_size), list(host_stride)
+    if math.prod(size) == 0:
+        return
+    info = restick_plan(size, src_layout, dst_layout) if stride == _contiguous_strides(size) else None
+    if info is not None:
+        dma_copy(src, dst, [info])
+        return
+    h2d_into(d2h_buffer(src, src_layout, size, stride), dst, dst_layout, stride)
+
+
+def relayout_buffer(src: torch.Tensor, host_size: Sequence[int], host_stride: Sequence[int],
+                    src_layout: SpyreTensorLayout, dst_layout: SpyreTensorLayout) -> torch.Tensor:
+    """A new buffer holding src's host values in dst_layout (see
+    ``relayout_into``); padding positions are zero."""
+    size, stride = list(host_size), list(host_stride)
+    if src_layout == dst_layout:  # the allocation byte for byte
+        dst = alloc_buffer(size, src.dtype, dst_layout, src.device, zero=False)
+        if dst.untyped_storage().nbytes() != src.untyped_storage().nbytes():
+            raise ValueError("relayout: src is not an allocation of its layout")
+        copy_buffer(src, dst)
+        return dst
+    info = restick_plan(size, src_layout, dst_layout) if stride == _contiguous_strides(size) else None
+    exact = info is not None and math.prod(info.size[: info.rank]) >= math.prod(dst_layout.device_size)
+    dst = alloc_buffer(size, src.dtype, dst_layout, src.device, zero=not exact)
+    if info is not None:
+        _check_layout_dtype(src.dtype, dst_layout)
+        dma_copy(src, dst, [info])
+    else:
+        relayout_into(src, dst, size, stride, src_layout, dst_layout)
+    return dst
 
 
 def transpose_restick_layout(rows: int, cols: int, dtype=torch.float16) -> SpyreTensorLayout:

@@ -136,3 +136,35 @@ def sdpa_overrideable(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
     seed = torch.empty((1,), dtype=torch.float16, device=query.device)
     offset = torch.empty((1,), dtype=torch.float16, device=query.device)
     return out, lse, None, None, query.shape[2], key.shape[2], seed, offset, None
+
+
+class sdpa_override(torch.overrides.TorchFunctionMode):
+    """Inside this context, ``torch.nn.functional.scaled_dot_product_attention``
+    calls this module can serve (CUDA float16 q / k / v, D in {64, 128},
+    Hq a multiple of Hkv, no dropout, masks of float16 / float32 / bool)
+    run the HIP kernels; any other call runs torch's own.
+
+    The reference gets the same effect by making ``_fused_sdp_choice``
+    answer "overrideable" for its device (torch_spyre/csrc/attn_utils.cpp:22-37);
+    CUDA tensors keep torch's choice outside this context."""
+
+    def __torch_function__(self, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func is torch.nn.functional.scaled_dot_product_attention and _servable(*args, **kwargs):
+            return scaled_dot_product_attention(*args, **kwargs)
+        return func(*args, **kwargs)
+
+
+def _servable(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None,
+              enable_gqa=False) -> bool:
+    ts = (query, key, value)
+    if not all(isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float16 and t.dim() == 4 for t in ts):
+        return False
+    if query.shape[-1] not in (64, 128) or key.shape[-1] != query.shape[-1] or dropout_p > 0.0:
+        return False
+    if key.shape[1] == 0 or query.shape[1] % key.shape[1] or (query.shape[1] != key.shape[1] and not enable_gqa):
+        return False
+    if attn_mask is not None and (is_causal or not isinstance(attn_mask, torch.Tensor)
+                                  or attn_mask.dtype not in _MASK_KIND):
+        return False
+    return True
