@@ -82,6 +82,25 @@ def sdpa_decomposition_fp64(q, k, v, scale=None, attn_mask=None, is_causal=False
     return out, lse
 
 
+def decode_lse_fp64(q, k, scale=None):
+    """The logsumexp of sdpa_decomposition_fp64 for one query token without
+    a mask, without forming P.V or expanding K over the group: q [Hq, D],
+    k [Hkv, S, D] -> [Hq] fp64.  The scale is applied to the score once
+    (the decomposition's sqrt(s) on q and on k multiplies to s)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    Hq, D = q.shape
+    Hkv = k.shape[0]
+    s = 1.0 / math.sqrt(D) if scale is None else scale
+    g = Hq // Hkv
+    out = np.empty(Hq)
+    for h in range(Hkv):
+        att = s * (q[h * g:(h + 1) * g] @ k[h].T)  # [g, S]
+        mx = att.max(axis=1)
+        out[h * g:(h + 1) * g] = mx + np.log(np.exp(att - mx[:, None]).sum(axis=1))
+    return out
+
+
 def sdpa_cpu_fp32(q, k, v, scale=None, attn_mask=None, is_causal=False) -> torch.Tensor:
     """torch CPU eager SDPA in fp32 (enable_gqa when Hq != Hkv).  Fully
     masked rows give zeros here (torch's safe softmax)."""

@@ -72,6 +72,55 @@ def oracle_rows(cache, table, lens, q, rows, scale):
     return OA.paged_decode_reference(q.cpu().float(), k_log, v_log, sub, lens.numpy(), scale, rows=rows)
 
 
+def oracle_lse64(cache, table, lens, q, rows, scale):
+    """fp64 logsumexp of scale q.k over each sampled row's tokens ([len(rows), Hq])."""
+    tab = table.cpu().numpy()
+    out = []
+    for b in rows:
+        n = max(1, (int(lens[b]) + 63) // 64)
+        idx = torch.tensor([int(p) for p in tab[b][:n]], dtype=torch.long, device=cache.k.device)
+        kd = cache.k.index_select(0, idx).cpu().numpy()
+        k_log, v_log = OA.pages_to_logical(kd, np.zeros_like(kd).reshape(-1), n, cache.Hkv, cache.D)
+        kb, _ = OA.gather_sequence(k_log, v_log, np.arange(n), int(lens[b]))
+        out.append(OA.decode_lse_fp64(q[b].cpu().numpy(), kb, scale=scale))
+    return np.stack(out)
+
+
+def mean_v64(cache, table, lens, Hq, rows):
+    """fp64 mean of V over each row's tokens, per q head ([len(rows), Hq, D]):
+    the attention output when every score is equal (q = 0)."""
+    tab = table.cpu().numpy()
+    out = []
+    for b in rows:
+        n = max(1, (int(lens[b]) + 63) // 64)
+        idx = torch.tensor([int(p) for p in tab[b][:n]], dtype=torch.long, device=cache.v.device)
+        vd = cache.v.index_select(0, idx)
+        _, v_log = OA.pages_to_logical(torch.zeros_like(vd).cpu().numpy(), vd.cpu().numpy(), n, cache.Hkv, cache.D)
+        _, vb = OA.gather_sequence(v_log, v_log, np.arange(n), int(lens[b]))
+        m = vb.astype(np.float64).mean(axis=1)  # [Hkv, D]
+        out.append(np.repeat(m, Hq // cache.Hkv, axis=0))
+    return np.stack(out)
+
+
+def assert_token_count_exact(out, lse, ref_mean, lens, rows):
+    """q = 0: every score is 0, P = 1 exactly and the row sum is exactly the
+    number of visible tokens, so LSE = ln(n) up to fp32 rounding of the log
+    (bound 4e-6, below ln(n / (n - 1)) for every n <= 131073) and out =
+    mean(V) up to its fp16 rounding (half an fp16 ulp + 1e-6; a lost or
+    doubled token moves some element of the mean by |v_t - mean| / n, several
+    fp16 ulps for the largest of the 128 * Hq features)."""
+    for i, b in enumerate(rows):
+        n = int(lens[b])
+        err = np.abs(lse[b].cpu().numpy().astype(np.float64) - math.log(n)).max()
+        assert err <= 4e-6 < math.log(n / (n - 1)), (b, n, err)
+        got = out[b].float().cpu().numpy().astype(np.float64)
+        ref = ref_mean[i]
+        # the spacing above |ref| (at a power of two the wider of the two binades)
+        tol = 0.5 * np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) + 1e-6
+        bad = np.abs(got - ref) > tol
+        assert not bad.any(), (b, n, int(bad.sum()), float(np.abs(got - ref).max()))
+
+
 def run(cache, table, lens, q, cuda, **kw):
     import torch_spyre_amd as tsa
 
@@ -91,6 +140,23 @@ def test_config1_dense_mha_vs_cpu_sdpa(cuda):
     assert_close(out, ref)
     ref64 = torch.from_numpy(OA.sdpa_decomposition_fp64(q.numpy(), k.numpy(), v.numpy(), 0.125))
     assert_close(out, ref64)
+
+
+def test_config1_token_count_exact(cuda):
+    """Config 1 through the SDPA kernels with q = 0 (closed form): LSE =
+    ln(512) and out = mean(V) over all 512 keys, for all 8 heads."""
+    import torch_spyre_amd as tsa
+
+    g = torch.Generator().manual_seed(SEED + 2)
+    v = torch.randn((1, 8, 512, 64), generator=g).half()
+    k = torch.randn((1, 8, 512, 64), generator=g).half()
+    out, lse = tsa.scaled_dot_product_attention(torch.zeros((1, 8, 1, 64), dtype=torch.float16, device=cuda),
+                                                k.to(cuda), v.to(cuda), scale=0.125, return_lse=True)
+    assert np.abs(lse.cpu().numpy().astype(np.float64) - math.log(512)).max() <= 4e-6
+    ref = v[0].double().mean(dim=1).numpy()  # [8, 64]
+    got = out[0, :, 0].float().cpu().numpy().astype(np.float64)
+    tol = 0.5 * np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) + 1e-6
+    assert (np.abs(got - ref) <= tol).all()
 
 
 @pytest.mark.parametrize("S", [1, 65, 513])
@@ -129,9 +195,23 @@ def test_config3_llama3_8b_full(cuda):
     permuted pool -- every row checked against the oracle."""
     B, Hq, Hkv, D, ctx = 32, 32, 8, 128, 4096
     cache, table, lens, q = make_case(cuda, B, Hq, Hkv, D, [ctx] * B, SEED)
-    out = run(cache, table, lens, q, cuda, max_context_len=ctx)
+    out, lse = run(cache, table, lens, q, cuda, max_context_len=ctx, return_lse=True)
     ref = oracle_rows(cache, table, lens, q, list(range(B)), 1 / math.sqrt(D))
     assert_close(out, ref)
+    # fp64 LSE of every row, bound 1e-4: below ln(4096 / 4095) = 2.4e-4, the
+    # shift one lost or doubled token of equal score would cause
+    lse64 = oracle_lse64(cache, table, lens, q, list(range(B)), 1 / math.sqrt(D))
+    assert np.abs(lse.cpu().numpy() - lse64).max() <= 1e-4 < math.log(4096 / 4095)
+
+
+def test_config3_token_count_exact(cuda):
+    """The Llama-3-8B shape with q = 0 (closed form): LSE = ln(4096) and
+    out = mean(V) for all 32 sequences."""
+    B, Hq, Hkv, D, ctx = 32, 32, 8, 128, 4096
+    cache, table, lens, q = make_case(cuda, B, Hq, Hkv, D, [ctx] * B, SEED + 1)
+    out, lse = run(cache, table, lens, torch.zeros_like(q), cuda, max_context_len=ctx, return_lse=True)
+    rows = list(range(B))
+    assert_token_count_exact(out, lse, mean_v64(cache, table, lens, Hq, rows), lens, rows)
 
 
 @pytest.mark.parametrize("split", [256, 64])
@@ -206,16 +286,34 @@ def test_page_permutation_invariance_bitexact(cuda):
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
 
 
-def test_config4_ragged_full_shape_sampled(cuda):
-    """64 sequences, ctx ~ U[128, 32768] (seeded), 32/8 heads, D 128, split 512
-    with the merge on every sequence; six sampled rows against the oracle."""
+def _config4_lens():
     g = torch.Generator().manual_seed(SEED)
-    lens = torch.randint(128, 32769, (64,), generator=g).tolist()
+    return torch.randint(128, 32769, (64,), generator=g).tolist()
+
+
+def test_config4_ragged_full_shape_all_rows(cuda):
+    """64 sequences, ctx ~ U[128, 32768] (seeded), 32/8 heads, D 128, split
+    512 (sequences over 4096 tokens go through the chunk partials and the
+    merge); every row against the oracle, LSE against fp64 (1e-4)."""
+    lens = _config4_lens()
     cache, table, lens_t, q = make_case(cuda, 64, 32, 8, 128, lens, SEED + 4)
-    out = run(cache, table, lens_t, q, cuda, split_tokens=512, max_context_len=max(lens))
-    rows = [0, 7, int(np.argmin(lens)), int(np.argmax(lens)), 40, 63]
-    ref = oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128))
-    assert_close(out[rows], ref)
+    out, lse = run(cache, table, lens_t, q, cuda, split_tokens=512, max_context_len=max(lens), return_lse=True)
+    rows = list(range(64))
+    for lo in range(0, 64, 16):
+        assert_close(out[lo:lo + 16], oracle_rows(cache, table, lens_t, q, rows[lo:lo + 16], 1 / math.sqrt(128)))
+    lse64 = oracle_lse64(cache, table, lens_t, q, rows, 1 / math.sqrt(128))
+    assert np.abs(lse.cpu().numpy() - lse64).max() <= 1e-4
+
+
+def test_config4_token_count_exact(cuda):
+    """The ragged batch with q = 0 (closed form): for every one of the 64
+    sequences LSE = ln(ctx) and out = mean(V)."""
+    lens = _config4_lens()
+    cache, table, lens_t, q = make_case(cuda, 64, 32, 8, 128, lens, SEED + 5)
+    out, lse = run(cache, table, lens_t, torch.zeros_like(q), cuda, split_tokens=512, max_context_len=max(lens),
+                   return_lse=True)
+    rows = list(range(64))
+    assert_token_count_exact(out, lse, mean_v64(cache, table, lens_t, 32, rows), lens_t, rows)
 
 
 def test_bad_page_id_gives_nan_not_fault(cuda):

@@ -11,7 +11,8 @@ from oracle import attention as OA
 from oracle import kv as OK
 from oracle import relayout as OR
 from tests.conftest import SEED
-from tests.test_attention_gpu import assert_close, make_case, oracle_rows, run
+from tests.test_attention_gpu import (assert_close, assert_token_count_exact, make_case, mean_v64, oracle_lse64,
+                                     oracle_rows, run)
 
 pytestmark = pytest.mark.gpu
 
@@ -84,7 +85,8 @@ def test_append_then_attend_matches_oracle(cuda):
 def test_config5_long_context_append_full_shape(cuda):
     """Batch 4, 64 q / 8 KV heads (g = 8), D 128: append the token at position
     131072 into its stick-layout page, then attend over 131073 tokens (2049
-    pages, several chunks and the merge pass); two rows against the oracle."""
+    pages, several chunks and the merge pass); every row against the oracle,
+    LSE against fp64, and the token count exact (q = 0)."""
     import torch_spyre_amd as tsa
 
     B, Hq, Hkv, D, ctx = 4, 64, 8, 128, 131072
@@ -94,6 +96,12 @@ def test_config5_long_context_append_full_shape(cuda):
     v_new = torch.randn((B, Hkv, D), generator=gg, device=cuda).half()
     pos = torch.full((B,), ctx, dtype=torch.int32, device=cuda)
     tsa.kv_append(k_new, v_new, cache.k, cache.v, table.to(cuda), pos)
-    out = run(cache, table, lens, q, cuda, max_context_len=ctx + 1)
-    rows = [0, 3]
-    assert_close(out[rows], oracle_rows(cache, table, lens, q, rows, 1 / math.sqrt(D)))
+    out, lse = run(cache, table, lens, q, cuda, max_context_len=ctx + 1, return_lse=True)
+    rows = list(range(B))
+    assert_close(out, oracle_rows(cache, table, lens, q, rows, 1 / math.sqrt(D)))
+    lse64 = oracle_lse64(cache, table, lens, q, rows, 1 / math.sqrt(D))
+    assert np.abs(lse.cpu().numpy() - lse64).max() <= 1e-4
+    # q = 0 (closed form): every one of the 131073 tokens, the appended one
+    # included, counted exactly once
+    out0, lse0 = run(cache, table, lens, torch.zeros_like(q), cuda, max_context_len=ctx + 1, return_lse=True)
+    assert_token_count_exact(out0, lse0, mean_v64(cache, table, lens, Hq, rows), lens, rows)

@@ -193,3 +193,17 @@ def test_fully_masked_row_nan_in_decomposition_zero_in_cpu_sdpa():
     assert np.isnan(OA.sdpa_decomposition_fp64(q, k, v, attn_mask=m)[0, 0, 1]).all()
     cpu = OA.sdpa_cpu_fp32(q, k, v, attn_mask=torch.from_numpy(m))
     assert not cpu[0, 0, 1].any()
+
+
+@pytest.mark.parametrize("Hq,Hkv,S,D,scale", [(8, 8, 300, 64, None), (32, 8, 77, 128, 0.3), (16, 2, 1, 128, 2.0)])
+def test_decode_lse_equals_decomposition_lse(Hq, Hkv, S, D, scale):
+    """The lean decode LSE equals the full decomposition's logsumexp; a
+    group mapping of h % Hkv (the plausible mistake) does not."""
+    q, k, v = _rand((1, Hq, 1, D), 30), _rand((1, Hkv, S, D), 31), _rand((1, Hkv, S, D), 32)
+    _, want = OA.sdpa_decomposition_fp64(q.numpy(), k.numpy(), v.numpy(), scale=scale, return_lse=True)
+    got = OA.decode_lse_fp64(q.numpy()[0, :, 0], k.numpy()[0], scale=scale)
+    assert np.allclose(got, want.reshape(-1), atol=1e-12, rtol=0)
+    if Hkv not in (1, Hq):
+        kk = k.numpy()[0][np.arange(Hq) % Hkv]  # [Hq, S, D], head h -> h % Hkv
+        wrong = OA.decode_lse_fp64(q.numpy()[0, :, 0], kk, scale=scale)
+        assert not np.allclose(wrong, want.reshape(-1), atol=1e-6)
