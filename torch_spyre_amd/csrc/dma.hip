@@ -2,7 +2,7 @@
 //
 // A loop nest says: for every index tuple i, dst[off_d + i.sd] = src[off_s + i.ss].
 // The host normalises it (drops unit loops, merges loops that are contiguous
-// on both sides) and picks one of three kernels:
+// on both sides) and picks one of four kinds of kernel:
 //
 //  * stick tile: one loop is a whole 128-byte stick, unit-stride on both
 //               sides, and two others continue it contiguously, one in dst
@@ -20,12 +20,20 @@
 //               whole cache lines on both sides.
 //  * transpose: one loop is unit-stride in src and another in dst (the stick
 //               moves to another dim, e.g. transpose-restick).  A wavefront
-//               owns four 64x64 tiles of 2-byte elements; each lane loads an
-//               8x8 block per tile as eight 16-byte row segments (all 32
-//               loads first), transposes them in registers and stores eight
-//               16-byte column segments per tile.  Loads and stores are both
-//               128-byte-line coalesced and LDS is not used.
+//               owns four 64x64 tiles of 2-byte elements (8x8 blocks of
+//               16 bytes); its loads (all 32 first) go straight into LDS,
+//               each lane then reads one 8x8 block per tile, transposes it
+//               in registers and stores eight 16-byte column segments.
+//               Loads and stores are both 128-byte-line coalesced.  4-byte
+//               elements, and nests with more than three outer loops, use
+//               a register-only form of the same tiling.
 //  * scalar:    anything else, element by element.
+//
+// Stick tiles and 2-byte transposes have a stepped form for nests of whole
+// tiles whose spans fit 32-bit buffer offsets (the common case): the tile
+// index is decomposed once, in 32-bit arithmetic, over only the loops
+// longer than one, from a kernel argument block sized to those loops, and
+// nothing is predicated.
 //
 // Index decomposition uses multiply-high division by loop-invariant divisors
 // (Granlund & Montgomery, "Division by Invariant Integers using
@@ -76,7 +84,7 @@ constexpr int kMaxLoops = SPYRE_MAX_RANK;
 constexpr int kThreads = 256;
 constexpr int kItems = 4;       // vec kernel: items per lane, strided by the block size
 constexpr int kTileSticks = 32; // stick tile: 32 x 32 sticks of 128 B per workgroup
-constexpr int kTilePad = 8;     // 16-B units of LDS padding per tile row (bank spread)
+constexpr int kAuxNT = 2;       // cache policy of a memory instruction: non-temporal
 constexpr int kTransposeTiles = 4;  // 64x64 tiles per wavefront
 
 struct Nest {
@@ -165,63 +173,257 @@ struct SNest {
   int64_t off_s, off_d;
 };
 
-// Moves one tile of kTileSticks x kTileSticks sticks: load k reads the B
-// run of A stick k (this lane: B stick `stick`, 16-byte unit `unit`) at
-// sp + k * a_ss; store k writes the A run of B stick k at dp + k * b_sd.
-// GUARDED: only A sticks < a_left and B sticks < b_left exist (b_lane /
-// a_lane: this lane's B / A stick exists).
-template <bool GUARDED>
-__device__ __forceinline__ void stick_tile(const char* sp, char* dp, int64_t a_ss, int64_t b_sd,
-                                           bool b_lane, bool a_lane, uint32_t a_left,
-                                           uint32_t b_left, u32x4* lds) {
-  constexpr int kRow = kTileSticks * 8 + kTilePad;  // LDS row: one B stick's A run, in 16-B units
-  const uint32_t stick = threadIdx.x >> 3, unit = threadIdx.x & 7;
-  u32x4 x[kTileSticks];
-#pragma unroll
-  for (int k = 0; k < kTileSticks; ++k, sp += a_ss)
-    if (!GUARDED || (b_lane && static_cast<uint32_t>(k) < a_left)) x[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sp));
-#pragma unroll
-  for (int k = 0; k < kTileSticks; ++k) lds[stick * kRow + k * 8 + unit] = x[k];
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kTileSticks; ++k) x[k] = lds[k * kRow + threadIdx.x];
-#pragma unroll
-  for (int k = 0; k < kTileSticks; ++k, dp += b_sd)
-    if (!GUARDED || (a_lane && static_cast<uint32_t>(k) < b_left)) __builtin_nontemporal_store(x[k], reinterpret_cast<u32x4*>(dp));
+// 16 bytes per lane from global memory straight into LDS: lane l of the
+// wavefront writes lds + 16 l (lds wave-uniform).  Non-temporal: every
+// byte is read once.
+__device__ __forceinline__ void load_lds16(const char* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(g), (__attribute__((address_space(3))) void*)lds,
+                                   16, 0, kAuxNT);
 }
 
+// The same through a buffer descriptor: base and extent in scalar
+// registers, a 32-bit per-lane byte offset (one VGPR) -- fewer address
+// instructions per load than 64-bit addresses.  kBufRange bounds the
+// offsets (the host checks that a tile's span fits).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kBufRange = 0x7ffffff0u;
+constexpr uint32_t kBufOob = 0x80000000u;  // an offset past kBufRange: the access is skipped
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit format
+
+__device__ __forceinline__ Rsrc make_rsrc(const char* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, kBufRange, kRsrcWord3);
+}
+
+__device__ __forceinline__ void load_lds16(Rsrc r, uint32_t off, char* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, kAuxNT);
+}
+
+__device__ __forceinline__ void store16(Rsrc r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kAuxNT);
+}
+
+// Descriptor of `range` bytes at base, and accesses whose offset is split
+// into a per-lane part (voff, a VGPR) and a wave-uniform part (soff, an
+// SGPR: one scalar add per access instead of a vector one).
+__device__ __forceinline__ Rsrc make_rsrc(const char* base, uint32_t range) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, range, kRsrcWord3);
+}
+
+__device__ __forceinline__ void load_lds16(Rsrc r, uint32_t voff, uint32_t soff, char* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, kAuxNT);
+}
+
+__device__ __forceinline__ void store16(Rsrc r, uint32_t voff, uint32_t soff, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, kAuxNT);
+}
+
+__device__ __forceinline__ void wait_loads() {
+  // s_waitcnt vmcnt(0); expcnt and lgkmcnt at their maxima (gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
+}
+
+constexpr int kStepLoops = 4;
+
+// The arguments of a stepped kernel: NL tile loops (the lengths and byte
+// strides of the loops a tile index decomposes into, fastest first), and
+// 32-bit offsets and descriptor ranges, the host having checked that each
+// side's span fits a buffer descriptor.
+template <int NL>
+struct StepNest {
+  uint32_t count;            // tiles (transpose: a multiple of kTransposeTiles)
+  uint32_t off_s, off_d;     // byte offsets of the nest in src / dst
+  uint32_t span_s, span_d;   // descriptor ranges (bytes)
+  uint32_t s1, s2;           // transpose: src stride of B, dst stride of A;
+                             // stick tile: src stride of A, dst stride of B
+  FastDiv loop[NL];
+  uint32_t ss[NL], sd[NL];
+};
+
+#define SPYRE_PIN_LOOP(k) "+s"(x.loop[k].d), "+s"(x.loop[k].mul), "+s"(x.loop[k].shift), "+s"(x.ss[k]), "+s"(x.sd[k])
+#define SPYRE_PIN_HEAD "+s"(src), "+s"(dst), "+s"(x.count), "+s"(x.off_s), "+s"(x.off_d), "+s"(x.span_s), \
+                       "+s"(x.span_d), "+s"(x.s1), "+s"(x.s2)
+// Every field and both base pointers in scalar registers, read in one
+// batch at entry (an argument read after another's wait costs a memory
+// round trip before the first load).
+template <int NL>
+__device__ __forceinline__ StepNest<NL> read_step(const StepNest<NL>& n, const char*& src, char*& dst) {
+  StepNest<NL> x = n;
+  if constexpr (NL == 1) {
+    asm volatile("" : SPYRE_PIN_HEAD, SPYRE_PIN_LOOP(0));
+  } else if constexpr (NL == 2) {
+    asm volatile("" : SPYRE_PIN_HEAD, SPYRE_PIN_LOOP(0), SPYRE_PIN_LOOP(1));
+  } else if constexpr (NL == 3) {
+    asm volatile("" : SPYRE_PIN_HEAD, SPYRE_PIN_LOOP(0), SPYRE_PIN_LOOP(1), SPYRE_PIN_LOOP(2));
+  } else {
+    static_assert(NL == 4, "1-4 tile loops");
+    asm volatile("" : SPYRE_PIN_HEAD, SPYRE_PIN_LOOP(0), SPYRE_PIN_LOOP(1), SPYRE_PIN_LOOP(2), SPYRE_PIN_LOOP(3));
+  }
+  return x;
+}
+#undef SPYRE_PIN_HEAD
+#undef SPYRE_PIN_LOOP
+
+// Byte offsets of tile q of a stepped nest (shift and mask when every loop
+// length is a power of two).
+template <int NL, bool POW2>
+__device__ __forceinline__ void step_offsets(const StepNest<NL>& x, uint32_t q, uint32_t& so, uint32_t& sd) {
+  so = x.off_s;
+  sd = x.off_d;
+#pragma unroll
+  for (int k = 0; k < NL; ++k) {
+    uint32_t q2, c;
+    if (POW2) {
+      c = q & (x.loop[k].d - 1);
+      q2 = q >> x.loop[k].shift;
+    } else {
+      q2 = fdiv(q, x.loop[k]);
+      c = q - q2 * x.loop[k].d;
+    }
+    so += c * x.ss[k];
+    sd += c * x.sd[k];
+    q = q2;
+  }
+}
+
+// Moves one tile of TA x TB sticks (128 KiB) through LDS.
+// Loads: 1 KiB chunk c (the 8 B sticks 8 (c % (TB / 8)) .. + 7 of A row
+// c / (TB / 8), contiguous in src) by wavefront c % 4, straight into LDS row
+// a (TB sticks, padded by 128 B so the store-side reads of neighbouring A
+// rows fall in different bank halves).
+// Stores: 1 KiB chunk m (the 8 A sticks 8 (m % (TA / 8)) .. + 7 of B stick
+// m / (TA / 8), contiguous in dst) by wavefront m % 4 (the four wavefronts
+// write neighbouring chunks of one run together), or, WAVE_RUNS, chunks
+// kPer w .. kPer (w + 1) - 1 by wavefront w (each writes whole runs).
+// GUARDED: only A sticks < a_left and B sticks < b_left exist.
+template <int TA, int TB, bool WAVE_RUNS, bool BUF, bool GUARDED>
+__device__ __forceinline__ void stick_tile(const char* sp, char* dp, int64_t a_ss, int64_t b_sd,
+                                           uint32_t a_left, uint32_t b_left, char* lds) {
+  constexpr int kRowB = TB * 128 + 128;
+  constexpr int kPer = TA * TB / 8 / 4;  // 1 KiB chunks per wavefront
+  static_assert(TA * TB == 1024 && TA % 8 == 0 && TB % 8 == 0, "128 KiB tiles of whole 1 KiB chunks");
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+  const int lane = static_cast<int>(threadIdx.x % 64);
+  const Rsrc rs = make_rsrc(sp);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int c = 4 * k + wave;
+    const int a = c / (TB / 8), b = (c % (TB / 8)) * 8 + lane / 8;
+    char* l = lds + a * kRowB + (c % (TB / 8)) * 1024;
+    if (!GUARDED || (static_cast<uint32_t>(a) < a_left && static_cast<uint32_t>(b) < b_left)) {
+      if (BUF)
+        load_lds16(rs, static_cast<uint32_t>(a) * static_cast<uint32_t>(a_ss) + b * 128 + (lane % 8) * 16, l);
+      else
+        load_lds16(sp + a * a_ss + b * 128 + (lane % 8) * 16, l);
+    }
+  }
+  wait_loads();
+  __syncthreads();
+  u32x4 x[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int m = WAVE_RUNS ? kPer * wave + k : 4 * k + wave;
+    const int b = m / (TA / 8), a = (m % (TA / 8)) * 8 + lane / 8;
+    x[k] = *reinterpret_cast<const u32x4*>(lds + a * kRowB + b * 128 + (lane % 8) * 16);
+  }
+  const Rsrc rd = make_rsrc(dp);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int m = WAVE_RUNS ? kPer * wave + k : 4 * k + wave;
+    const int b = m / (TA / 8), a = (m % (TA / 8)) * 8 + lane / 8;
+    if (!GUARDED || (static_cast<uint32_t>(a) < a_left && static_cast<uint32_t>(b) < b_left)) {
+      if (BUF)
+        store16(rd, static_cast<uint32_t>(b) * static_cast<uint32_t>(b_sd) + a * 128 + (lane % 8) * 16, x[k]);
+      else
+        __builtin_nontemporal_store(x[k], reinterpret_cast<u32x4*>(dp + b * b_sd + a * 128 + (lane % 8) * 16));
+    }
+  }
+}
+
+// BUF: the tile's spans fit 32-bit buffer offsets (checked on the host).
+template <int TA, int TB, bool WAVE_RUNS, bool BUF>
 __global__ __launch_bounds__(kThreads) void dma_stick_tile_kernel(const char* __restrict__ src,
                                                                    char* __restrict__ dst, SNest n) {
-  __shared__ u32x4 lds[kTileSticks * (kTileSticks * 8 + kTilePad)];
-  const uint32_t na = pinned(n.na), nb = pinned(n.nb);
-  const int64_t a_ss = pinned(n.a_ss), b_sd = pinned(n.b_sd);
+  __shared__ __align__(16) char lds[TA * (TB * 128 + 128)];
+  // Every argument of the tile decomposition read by one statement: all the
+  // reads are issued at entry and waited for once (an argument read after
+  // another's wait costs a memory round trip before the first load).
+  uint32_t na = n.na, nb = n.nb, nouter = n.nouter, b_first = n.b_first;
+  int64_t a_ss = n.a_ss, b_sd = n.b_sd, so = n.off_s, sd = n.off_d;
+  FastDiv dx = n.tiles_x, dy = n.tiles_y;
+  asm volatile("" : "+s"(na), "+s"(nb), "+s"(nouter), "+s"(b_first), "+s"(a_ss), "+s"(b_sd), "+s"(so), "+s"(sd),
+               "+s"(dx.d), "+s"(dx.mul), "+s"(dx.shift), "+s"(dy.d), "+s"(dy.mul), "+s"(dy.shift));
   uint32_t q = blockIdx.x;
-  uint32_t q2 = fdiv(q, n.tiles_x);
-  const uint32_t tx = q - q2 * n.tiles_x.d;
+  uint32_t q2 = fdiv(q, dx);
+  const uint32_t tx = q - q2 * dx.d;
   q = q2;
-  q2 = fdiv(q, n.tiles_y);
-  const uint32_t ty = q - q2 * n.tiles_y.d;
+  q2 = fdiv(q, dy);
+  const uint32_t ty = q - q2 * dy.d;
   q = q2;
-  const uint32_t ta = n.b_first ? ty : tx, tb = n.b_first ? tx : ty;
-  int64_t so = n.off_s, sd = n.off_d;
-  for (int k = 0; k < n.nouter; ++k) {
+  const uint32_t ta = b_first ? ty : tx, tb = b_first ? tx : ty;
+  for (uint32_t k = 0; k < nouter; ++k) {
     q2 = fdiv(q, n.outer[k]);
     const int64_t c = q - q2 * n.outer[k].d;
     so += c * n.ss[k];
     sd += c * n.sd[k];
     q = q2;
   }
-  const uint32_t a0 = ta * kTileSticks, b0 = tb * kTileSticks;
-  const uint32_t stick = threadIdx.x >> 3, unit = threadIdx.x & 7;
-  const char* sp = src + so + static_cast<int64_t>(a0) * a_ss + static_cast<int64_t>(b0 + stick) * 128 + unit * 16;
-  char* dp = dst + sd + static_cast<int64_t>(b0) * b_sd + static_cast<int64_t>(a0 + stick) * 128 + unit * 16;
+  const uint32_t a0 = ta * TA, b0 = tb * TB;
+  const char* sp = src + so + static_cast<int64_t>(a0) * a_ss + static_cast<int64_t>(b0) * 128;
+  char* dp = dst + sd + static_cast<int64_t>(b0) * b_sd + static_cast<int64_t>(a0) * 128;
   // Edge tiles predicate every access; full tiles (all but the last along A
-  // and B) run unpredicated, so their LDS writes follow the loads as the
-  // data arrives.
-  if (a0 + kTileSticks <= na && b0 + kTileSticks <= nb)
-    stick_tile<false>(sp, dp, a_ss, b_sd, true, true, 0, 0, lds);
+  // and B) run unpredicated.
+  if (a0 + TA <= na && b0 + TB <= nb)
+    stick_tile<TA, TB, WAVE_RUNS, BUF, false>(sp, dp, a_ss, b_sd, 0, 0, lds);
   else
-    stick_tile<true>(sp, dp, a_ss, b_sd, b0 + stick < nb, a0 + stick < na, na - a0, nb - b0, lds);
+    stick_tile<TA, TB, WAVE_RUNS, BUF, true>(sp, dp, a_ss, b_sd, na - a0, nb - b0, lds);
+}
+
+// The stepped form of dma_stick_tile_kernel: every tile whole, both spans
+// within one buffer descriptor, the tile index decomposed over the tile
+// loops (B tiles, A tiles, the outer loops; those longer than one) in
+// 32-bit arithmetic.  Every access's per-lane offset is lane * 16 -- the
+// eight lanes of a stick and the eight sticks of a 1 KiB chunk are
+// contiguous on both sides -- and the rest is a scalar offset.
+// (Storing the first half of a tile while its second half loads was
+// measured no faster on fp16 [4096, 4096] in either direction -- the two
+// streams share the same HBM -- and slower where the halves split 4 KiB
+// src runs.)
+template <int TA, int TB, bool WAVE_RUNS, int NL, bool POW2>
+__global__ __launch_bounds__(kThreads) void dma_stick_step_kernel(const char* __restrict__ src_arg,
+                                                                  char* __restrict__ dst_arg, StepNest<NL> n) {
+  constexpr int kRowB = TB * 128 + 128;
+  constexpr int kPer = TA * TB / 8 / 4;  // 1 KiB chunks per wavefront
+  static_assert(TA * TB == 1024 && TA % 8 == 0 && TB % 8 == 0, "128 KiB tiles of whole 1 KiB chunks");
+  __shared__ __align__(16) char lds[TA * kRowB];
+  const char* src = src_arg;
+  char* dst = dst_arg;
+  const StepNest<NL> x = read_step(n, src, dst);
+  const uint32_t a_ss = x.s1, b_sd = x.s2;
+  uint32_t so, sd;
+  step_offsets<NL, POW2>(x, blockIdx.x, so, sd);
+  const Rsrc rs = make_rsrc(src, x.span_s), rd = make_rsrc(dst, x.span_d);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t lane = threadIdx.x % 64, v = lane * 16;
+  // load chunk c: A row c / (TB / 8), sticks 8 (c % (TB / 8)) .. + 7
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t c = 4 * k + wave, a = c / (TB / 8), cb = c % (TB / 8);
+    load_lds16(rs, v, so + a * a_ss + cb * 1024, lds + a * kRowB + cb * 1024);
+  }
+  wait_loads();
+  __syncthreads();
+  // store chunk m: B stick m / (TA / 8), A sticks 8 (m % (TA / 8)) .. + 7
+  u32x4 r[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t m = WAVE_RUNS ? kPer * wave + k : 4 * k + wave, b = m / (TA / 8), ca = m % (TA / 8);
+    r[k] = *reinterpret_cast<const u32x4*>(lds + (ca * 8 + lane / 8) * kRowB + b * 128 + (lane % 8) * 16);
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t m = WAVE_RUNS ? kPer * wave + k : 4 * k + wave, b = m / (TA / 8), ca = m % (TA / 8);
+    store16(rd, v, sd + b * b_sd + ca * 1024, r[k]);
+  }
 }
 
 // Transpose nest: loop A is unit-stride in src, loop B unit-stride in dst.
@@ -330,6 +532,202 @@ __global__ __launch_bounds__(kThreads) void dma_transpose_kernel(const char* __r
     transpose_tiles<ESZ, true>(src, dst, n, so, sd, ok);
 }
 
+// 2-byte transposes through LDS: a wavefront's kTransposeTiles 64 x 64 tiles
+// travel from memory straight into LDS (each load instruction: 8 B rows of
+// one tile, 128 contiguous bytes each), then every lane reads its 8 x 8
+// block of each tile (row r at (r / 8) * 1152 + (r % 8) * 128, 8-row groups
+// padded so that the eight groups a read touches fall in different bank
+// halves), transposes it in registers and stores as dma_transpose_kernel.
+// Measured on fp16 [4096, 4096] transpose-restick (tiles 8 KiB contiguous
+// on both sides): 11.2 -> 10.9 us against the register-only kernel.
+constexpr int kTrGroupB = 8 * 128 + 128;
+constexpr int kTrTileB = 8 * kTrGroupB;
+
+// NOUT: the number of outer loops, or -1 for any count (generic path).
+// The prologue is straight-line code ending in one register barrier over
+// everything the loads and stores use, so every argument is read in one
+// batch at entry and all four tiles' offsets exist before the first load.
+// (Arguments read in rounds -- here the loop sizes after the tile counts --
+// each cost a memory round trip before the first load: measured 12.1 ->
+// 11.1 us on the [4096, 4096] transpose-restick.)
+// The arguments of a transpose nest with NOUT (0-3) outer loops, read into
+// scalar registers by one statement: every read is issued at entry and
+// waited for once.
+template <int NOUT>
+struct TArgs {
+  uint32_t na, nb, tiles;
+  FastDiv da, db, od[NOUT > 0 ? NOUT : 1];
+  int64_t ss[NOUT > 0 ? NOUT : 1], sd[NOUT > 0 ? NOUT : 1];
+  int64_t a_sd, b_ss, off_s, off_d;
+};
+
+#define SPYRE_PIN_DIV(f) "+s"(f.d), "+s"(f.mul), "+s"(f.shift)
+template <int NOUT>
+__device__ __forceinline__ TArgs<NOUT> read_targs(const TNest& n) {
+  TArgs<NOUT> x;
+  x.na = n.na;
+  x.nb = n.nb;
+  x.tiles = n.tiles;
+  x.da = n.tiles_a;
+  x.db = n.tiles_b;
+  for (int k = 0; k < (NOUT > 0 ? NOUT : 1); ++k) {
+    x.od[k] = n.outer[k];
+    x.ss[k] = n.ss[k];
+    x.sd[k] = n.sd[k];
+  }
+  x.a_sd = n.a_sd;
+  x.b_ss = n.b_ss;
+  x.off_s = n.off_s;
+  x.off_d = n.off_d;
+  if constexpr (NOUT <= 1) {
+    asm volatile("" : "+s"(x.na), "+s"(x.nb), "+s"(x.tiles), SPYRE_PIN_DIV(x.da), SPYRE_PIN_DIV(x.db),
+                 SPYRE_PIN_DIV(x.od[0]), "+s"(x.ss[0]), "+s"(x.sd[0]), "+s"(x.a_sd), "+s"(x.b_ss), "+s"(x.off_s),
+                 "+s"(x.off_d));
+  } else if constexpr (NOUT == 2) {
+    asm volatile("" : "+s"(x.na), "+s"(x.nb), "+s"(x.tiles), SPYRE_PIN_DIV(x.da), SPYRE_PIN_DIV(x.db),
+                 SPYRE_PIN_DIV(x.od[0]), SPYRE_PIN_DIV(x.od[1]), "+s"(x.ss[0]), "+s"(x.sd[0]), "+s"(x.ss[1]),
+                 "+s"(x.sd[1]), "+s"(x.a_sd), "+s"(x.b_ss), "+s"(x.off_s), "+s"(x.off_d));
+  } else {
+    static_assert(NOUT == 3, "read_targs serves 0-3 outer loops");
+    asm volatile("" : "+s"(x.na), "+s"(x.nb), "+s"(x.tiles), SPYRE_PIN_DIV(x.da), SPYRE_PIN_DIV(x.db),
+                 SPYRE_PIN_DIV(x.od[0]), SPYRE_PIN_DIV(x.od[1]), SPYRE_PIN_DIV(x.od[2]), "+s"(x.ss[0]),
+                 "+s"(x.sd[0]), "+s"(x.ss[1]), "+s"(x.sd[1]), "+s"(x.ss[2]), "+s"(x.sd[2]), "+s"(x.a_sd),
+                 "+s"(x.b_ss), "+s"(x.off_s), "+s"(x.off_d));
+  }
+  return x;
+}
+#undef SPYRE_PIN_DIV
+
+// NOUT: the number of outer loops (0-3).  Every argument is read in one
+// batch at entry (read_targs); each tile's loads are issued as soon as its
+// offsets are known.  (Arguments read in rounds -- the loop sizes after the
+// tile counts -- each cost a memory round trip before the first load, and a
+// prologue that computed all four tiles before loading delayed the chip's
+// first reads: 12.1 -> 11.2 us on the [4096, 4096] transpose-restick.)
+// BUF: the loads use a per-tile buffer descriptor (64 rows of b_ss fit
+// 32-bit offsets, checked on the host).
+template <int NOUT, bool BUF>
+__global__ __launch_bounds__(kThreads) void dma_transpose_lds_kernel(const char* __restrict__ src,
+                                                                     char* __restrict__ dst, TNest n) {
+  __shared__ __align__(16) char lds[kThreads / 64 * kTransposeTiles * kTrTileB];
+  const TArgs<NOUT> x = read_targs<NOUT>(n);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t wave = blockIdx.x * (kThreads / 64) + wv;
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t na = x.na, nb = x.nb;
+  const int64_t b_ss = x.b_ss, a_sd = x.a_sd;
+  char* wl = lds + wv * kTransposeTiles * kTrTileB;
+  int64_t sd[kTransposeTiles];
+  uint32_t ta[kTransposeTiles], tb[kTransposeTiles];
+  bool in[kTransposeTiles], whole[kTransposeTiles];
+#pragma unroll
+  for (int t = 0; t < kTransposeTiles; ++t) {
+    const uint32_t tile = wave * kTransposeTiles + t;
+    uint32_t q = fdiv(tile, x.da);
+    ta[t] = tile - q * x.da.d;
+    uint32_t q2 = fdiv(q, x.db);
+    tb[t] = q - q2 * x.db.d;
+    q = q2;
+    int64_t so = x.off_s, d = x.off_d;
+#pragma unroll
+    for (int k = 0; k < NOUT; ++k) {
+      q2 = fdiv(q, x.od[k]);
+      const int64_t c = q - q2 * x.od[k].d;
+      so += c * x.ss[k];
+      d += c * x.sd[k];
+      q = q2;
+    }
+    sd[t] = d;
+    in[t] = tile < x.tiles;
+    whole[t] = in[t] && ta[t] * 8 + 8 <= na && tb[t] * 8 + 8 <= nb;  // wave-uniform
+    // Loads: group g is src rows 8 (8 tb + g) .. + 7 (this lane: row + lane
+    // / 8) of A block 8 ta + lane % 8, into LDS group g.
+    const uint32_t ablk = ta[t] * 8 + lane % 8;
+    const char* tbase = src + so + static_cast<int64_t>(ta[t]) * 128 + static_cast<int64_t>(64 * tb[t]) * b_ss;
+    const Rsrc rs = make_rsrc(tbase);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      char* l = wl + t * kTrTileB + g * kTrGroupB;
+      const bool ok = whole[t] | (in[t] & (ablk < na) & (tb[t] * 8 + g < nb));
+      if (BUF) {
+        // a lane outside the nest gets an offset past the descriptor's
+        // range: the load is skipped (its LDS slot feeds no store), no branch
+        const uint32_t off = (lane % 8) * 16 + static_cast<uint32_t>(8 * g + lane / 8) * static_cast<uint32_t>(b_ss);
+        load_lds16(rs, ok ? off : kBufOob, l);
+      } else if (ok) {
+        load_lds16(tbase + (lane % 8) * 16 + static_cast<int64_t>(8 * g + lane / 8) * b_ss, l);
+      }
+    }
+  }
+  wait_loads();
+  // This lane's block: A block 8 ta + lane % 8, B block 8 tb + lane / 8.
+  const uint32_t la = lane % 8, lb = lane / 8;
+#pragma unroll
+  for (int t = 0; t < kTransposeTiles; ++t) {
+    u32x4 r[8], o[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+      r[b] = *reinterpret_cast<const u32x4*>(wl + t * kTrTileB + lb * kTrGroupB + b * 128 + la * 16);
+    spyre_hip::transpose8x8_b16(r, o);
+    const uint32_t ablk = ta[t] * 8 + la, sb = tb[t] * 8 + lb;
+    if (whole[t] || (in[t] && ablk < na && sb < nb)) {
+      char* dp = dst + sd[t] + static_cast<int64_t>(sb) * 16 + static_cast<int64_t>(ablk) * 8 * a_sd;
+#pragma unroll
+      for (int a = 0; a < 8; ++a) __builtin_nontemporal_store(o[a], reinterpret_cast<u32x4*>(dp + a * a_sd));
+    }
+  }
+}
+
+// The stepped form of dma_transpose_lds_kernel, for nests whose tiles are
+// all whole, whose tile count is a multiple of kTransposeTiles, whose src
+// and dst spans fit one buffer descriptor each, and whose tiles of one
+// wavefront lie along one loop (all checked on the host).  The tile loops
+// -- A tiles, B tiles and the outer loops, those longer than one, the first
+// of them the one a wavefront's tiles step along -- are decomposed once per
+// wavefront in 32-bit arithmetic (shift and mask when every loop length is
+// a power of two), each load and store adds a scalar offset to a per-lane
+// one, and nothing is predicated.  The prologue before the first load is
+// what this saves: the general kernel decomposes every tile with 64-bit
+// multiply-adds, ~80 scalar instructions between one tile's loads and the
+// next.
+template <int NL, bool POW2>
+__global__ __launch_bounds__(kThreads) void dma_transpose_step_kernel(const char* __restrict__ src_arg,
+                                                                      char* __restrict__ dst_arg, StepNest<NL> n) {
+  __shared__ __align__(16) char lds[kThreads / 64 * kTransposeTiles * kTrTileB];
+  const char* src = src_arg;
+  char* dst = dst_arg;
+  const StepNest<NL> x = read_step(n, src, dst);
+  const uint32_t b_ss = x.s1, a_sd = x.s2;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t tile = (blockIdx.x * (kThreads / 64) + wv) * kTransposeTiles;
+  if (tile >= x.count) return;  // wave-uniform; no barrier follows
+  uint32_t so, sd;
+  step_offsets<NL, POW2>(x, tile, so, sd);
+  const Rsrc rs = make_rsrc(src, x.span_s), rd = make_rsrc(dst, x.span_d);
+  const uint32_t lane = threadIdx.x % 64, la = lane % 8, lb = lane / 8;
+  char* wl = lds + wv * kTransposeTiles * kTrTileB;
+  // load group g of a tile: its src rows 8 g + lb, bytes la * 16 of each
+  const uint32_t vs = la * 16 + lb * b_ss;
+#pragma unroll
+  for (int t = 0; t < kTransposeTiles; ++t)
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+      load_lds16(rs, vs, so + t * x.ss[0] + 8 * g * b_ss, wl + t * kTrTileB + g * kTrGroupB);
+  wait_loads();
+  // store a of this lane's block: dst row 8 la + a of the tile, bytes lb * 16
+  const uint32_t vd = lb * 16 + la * 8 * a_sd;
+#pragma unroll
+  for (int t = 0; t < kTransposeTiles; ++t) {
+    u32x4 r[8], o[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+      r[b] = *reinterpret_cast<const u32x4*>(wl + t * kTrTileB + lb * kTrGroupB + b * 128 + la * 16);
+    spyre_hip::transpose8x8_b16(r, o);
+#pragma unroll
+    for (int a = 0; a < 8; ++a) store16(rd, vd, sd + t * x.sd[0] + a * a_sd, o[a]);
+  }
+}
+
 template <int ESZ>
 __global__ __launch_bounds__(kThreads) void dma_scalar_kernel(const char* __restrict__ src,
                                                               char* __restrict__ dst, Nest n) {
@@ -364,6 +762,47 @@ std::vector<Loop> normalise(const spyre_stride_info& info, int esz) {
 }
 
 bool aligned(const void* p, int64_t v) { return reinterpret_cast<uintptr_t>(p) % v == 0; }
+
+template <int NL>
+StepNest<NL> make_step(const std::vector<Loop>& tl, int64_t count, int64_t off_s, int64_t off_d, int64_t span_s,
+                       int64_t span_d, int64_t s1, int64_t s2) {
+  StepNest<NL> x{};
+  x.count = static_cast<uint32_t>(count);
+  x.off_s = static_cast<uint32_t>(off_s);
+  x.off_d = static_cast<uint32_t>(off_d);
+  x.span_s = static_cast<uint32_t>(span_s);
+  x.span_d = static_cast<uint32_t>(span_d);
+  x.s1 = static_cast<uint32_t>(s1);
+  x.s2 = static_cast<uint32_t>(s2);
+  for (int k = 0; k < NL; ++k) {
+    x.loop[k] = make_fastdiv(static_cast<uint32_t>(tl[k].size));
+    x.ss[k] = static_cast<uint32_t>(tl[k].ss);
+    x.sd[k] = static_cast<uint32_t>(tl[k].sd);
+  }
+  return x;
+}
+
+// The span checks of a stepped nest: strides non-negative, every loop
+// length a power of two or not, and the byte extent of each side, given the
+// extent of one tile.
+struct StepSpan {
+  bool ok = true, pow2 = true;
+  int64_t span_s = 0, span_d = 0;
+};
+StepSpan step_span(const std::vector<Loop>& tl, int64_t off_s, int64_t off_d, int64_t tile_s, int64_t tile_d) {
+  StepSpan r;
+  r.ok = !tl.empty() && static_cast<int>(tl.size()) <= kStepLoops && off_s >= 0 && off_d >= 0;
+  r.span_s = off_s + tile_s;
+  r.span_d = off_d + tile_d;
+  for (const Loop& l : tl) {
+    r.ok = r.ok && l.ss >= 0 && l.sd >= 0;
+    r.span_s += (l.size - 1) * l.ss;
+    r.span_d += (l.size - 1) * l.sd;
+    r.pow2 = r.pow2 && (l.size & (l.size - 1)) == 0;
+  }
+  r.ok = r.ok && r.span_s <= int64_t{kBufRange} && r.span_d <= int64_t{kBufRange};
+  return r;
+}
 
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -452,13 +891,21 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
         SNest n{};
         n.na = static_cast<uint32_t>(outer[ai].size);
         n.nb = static_cast<uint32_t>(outer[bi].size);
-        const uint32_t ta = (n.na + kTileSticks - 1) / kTileSticks;
-        const uint32_t tb = (n.nb + kTileSticks - 1) / kTileSticks;
+        // Tile shape: 32 x 32 sticks; 64 x 16 when the 64 A sticks are a
+        // whole dst row that B continues (sticks -> row-major of 8 KiB
+        // rows): a workgroup then writes 128 KiB of contiguous dst and each
+        // wavefront a quarter of it (measured: 11.4 -> 11.0 us on fp16
+        // [4096, 4096]; the 32 x 32 tile with interleaved stores is best for
+        // row-major -> sticks).
+        const bool tall = n.na == 64 && outer[bi].sd == 64 * row;
+        const uint32_t TA = tall ? 64 : kTileSticks, TB = tall ? 16 : kTileSticks;
+        const uint32_t ta = (n.na + TA - 1) / TA;
+        const uint32_t tb = (n.nb + TB - 1) / TB;
         int64_t tiles = int64_t{ta} * tb;
-        // Consecutive workgroups step along the loop whose other-side stride
-        // is smaller (the row-major rows), so concurrently running tiles
-        // cover neighbouring memory on both sides.
-        n.b_first = outer[bi].sd < outer[ai].ss;
+        // Consecutive workgroups step along B, the loop contiguous in src:
+        // neighbouring tiles read neighbouring memory (measured: ~1 %
+        // faster than stepping along A on row-major -> sticks).
+        n.b_first = 1;
         n.tiles_x = make_fastdiv(n.b_first ? tb : ta);
         n.tiles_y = make_fastdiv(n.b_first ? ta : tb);
         n.a_ss = outer[ai].ss;
@@ -473,8 +920,48 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
           ++n.nouter;
           tiles *= outer[k].size;
         }
+        // Stepped kernel: whole tiles, spans within a descriptor.
+        std::vector<Loop> tl;
+        if (tb > 1) tl.push_back({tb, int64_t{TB} * row, int64_t{TB} * n.b_sd});
+        if (ta > 1) tl.push_back({ta, int64_t{TA} * n.a_ss, int64_t{TA} * row});
+        for (int k = 0; k < n.nouter; ++k) tl.push_back({n.outer[k].d, n.ss[k], n.sd[k]});
+        const StepSpan sp = step_span(tl, off_s, off_d, (int64_t{TA} - 1) * n.a_ss + int64_t{TB} * row,
+                                      (int64_t{TB} - 1) * n.b_sd + int64_t{TA} * row);
+        if (sp.ok && n.na % TA == 0 && n.nb % TB == 0 && n.a_ss > 0 && n.b_sd > 0 && tiles < (int64_t{1} << 31)) {
+          const dim3 grid(static_cast<uint32_t>(tiles));
+          auto step_go = [&](auto nl_c) {
+            constexpr int NL = decltype(nl_c)::value;
+            const StepNest<NL> x = make_step<NL>(tl, tiles, off_s, off_d, sp.span_s, sp.span_d, n.a_ss, n.b_sd);
+            if (tall && sp.pow2)
+              dma_stick_step_kernel<64, 16, true, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (tall)
+              dma_stick_step_kernel<64, 16, true, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (sp.pow2)
+              dma_stick_step_kernel<32, 32, false, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else
+              dma_stick_step_kernel<32, 32, false, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
+          };
+          switch (tl.size()) {
+            case 1: step_go(std::integral_constant<int, 1>{}); break;
+            case 2: step_go(std::integral_constant<int, 2>{}); break;
+            case 3: step_go(std::integral_constant<int, 3>{}); break;
+            default: step_go(std::integral_constant<int, 4>{}); break;
+          }
+          return check_launch("dma_stick_step_kernel");
+        }
         if (tiles < (int64_t{1} << 31)) {
-          dma_stick_tile_kernel<<<dim3(static_cast<uint32_t>(tiles)), kThreads, 0, st>>>(src, dst, n);
+          const dim3 grid(static_cast<uint32_t>(tiles));
+          // 32-bit buffer offsets when a tile's spans fit them
+          const bool buf = (int64_t{TA} - 1) * n.a_ss + int64_t{TB} * row < int64_t{kBufRange} &&
+                           (int64_t{TB} - 1) * n.b_sd + int64_t{TA} * row < int64_t{kBufRange};
+          if (tall && buf)
+            dma_stick_tile_kernel<64, 16, true, true><<<grid, kThreads, 0, st>>>(src, dst, n);
+          else if (tall)
+            dma_stick_tile_kernel<64, 16, true, false><<<grid, kThreads, 0, st>>>(src, dst, n);
+          else if (buf)
+            dma_stick_tile_kernel<32, 32, false, true><<<grid, kThreads, 0, st>>>(src, dst, n);
+          else
+            dma_stick_tile_kernel<32, 32, false, false><<<grid, kThreads, 0, st>>>(src, dst, n);
           return check_launch("dma_stick_tile_kernel");
         }
       }
@@ -539,6 +1026,32 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
       n.tiles = static_cast<uint32_t>(tiles);
       constexpr uint32_t per_block = kThreads / 64 * kTransposeTiles;
       const dim3 grid((n.tiles + per_block - 1) / per_block);
+      if (esz == 2) {
+        // the stepped kernel's tile loops: A tiles, B tiles, the outer loops
+        std::vector<Loop> tl;
+        if (ta > 1) tl.push_back({ta, 128, 64 * A.sd});
+        if (tb > 1) tl.push_back({tb, 64 * B.ss, 128});
+        for (const Loop& o : outer) tl.push_back(o);
+        const StepSpan sp = step_span(tl, off_s, off_d, 63 * B.ss + 128, 63 * A.sd + 128);
+        if (sp.ok && n.na % 8 == 0 && n.nb % 8 == 0 && tl[0].size % kTransposeTiles == 0 && A.sd > 0 &&
+            B.ss > 0) {
+          auto step_go = [&](auto nl_c) {
+            constexpr int NL = decltype(nl_c)::value;
+            const StepNest<NL> x = make_step<NL>(tl, n.tiles, off_s, off_d, sp.span_s, sp.span_d, B.ss, A.sd);
+            if (sp.pow2)
+              dma_transpose_step_kernel<NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else
+              dma_transpose_step_kernel<NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
+          };
+          switch (tl.size()) {
+            case 1: step_go(std::integral_constant<int, 1>{}); break;
+            case 2: step_go(std::integral_constant<int, 2>{}); break;
+            case 3: step_go(std::integral_constant<int, 3>{}); break;
+            default: step_go(std::integral_constant<int, 4>{}); break;
+          }
+          return check_launch("dma_transpose_step_kernel");
+        }
+      }
       auto go = [&](auto esz_c, auto nout_c) {
         dma_transpose_kernel<decltype(esz_c)::value, decltype(nout_c)::value>
             <<<grid, kThreads, 0, st>>>(src, dst, n);
@@ -554,10 +1067,31 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
           default: go(esz_c, std::integral_constant<int, -1>{}); break;
         }
       };
-      if (esz == 2)
+      if (esz == 2 && n.nouter <= 3) {
+        // LDS-staged loads for 2-byte tiles (one 147 KiB workgroup per CU);
+        // a tile's 64 rows in 32-bit buffer offsets when they fit
+        const bool buf = 64 * n.b_ss + 128 < int64_t{kBufRange};
+        auto lds_go = [&](auto nout_c, auto buf_c) {
+          dma_transpose_lds_kernel<decltype(nout_c)::value, decltype(buf_c)::value>
+              <<<grid, kThreads, 0, st>>>(src, dst, n);
+        };
+        auto by_buf = [&](auto nout_c) {
+          if (buf)
+            lds_go(nout_c, std::true_type{});
+          else
+            lds_go(nout_c, std::false_type{});
+        };
+        switch (n.nouter) {
+          case 0: by_buf(std::integral_constant<int, 0>{}); break;
+          case 1: by_buf(std::integral_constant<int, 1>{}); break;
+          case 2: by_buf(std::integral_constant<int, 2>{}); break;
+          default: by_buf(std::integral_constant<int, 3>{}); break;
+        }
+      } else if (esz == 2) {
         by_nout(I2{});
-      else
+      } else {
         by_nout(I4{});
+      }
       return check_launch("dma_transpose_kernel");
     }
   }
