@@ -12,7 +12,8 @@ two KV caches (1.07 GB) alternate so the 256 MB last-level cache cannot
 serve a step from the previous one.
 
 Also timed: under "more_configs", the dense MHA decode call (q [1, 8, 1, 64], k/v
-[1, 8, 512, 64]; absolute µs, launch-bound), the Llama-3-8B decode step through SDPA
+[1, 8, 512, 64]; absolute µs, launch-bound; eager, and prepared once as SdpaCall), the
+Llama-3-8B decode step through SDPA
 with dense K/V (q [32, 32, 1, 128], k/v [32, 8, 4096, 128]), its batch-1 (absolute µs)
 and long-context (q [4, 64, 1, 128], k/v [4, 8, 32768, 128]) counterparts, the ragged batch (64 sequences, context
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
@@ -160,12 +161,15 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     gg = torch.Generator(device=dev).manual_seed(seed + 1)
 
     # dense MHA decode: q [1, 8, 1, 64], k/v [1, 8, 512, 64], scale 1/8 (launch-bound:
-    # absolute µs; one SDPA forward kernel)
+    # absolute µs; 8 key splits of one 64-key step, then the merge kernel)
     q1 = torch.randn((1, 8, 1, 64), generator=gg, device=dev).half()
     k1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
     v1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
     ms = timed(lambda i: tsa.sdpa_decode(q1, k1, v1, scale=0.125), steps, warmup, stream)
+    call1 = tsa.SdpaCall(q1, k1, v1, scale=0.125)  # validated once, as a serving loop holds it
+    ms_p = timed(lambda i: call1(), steps, warmup, stream)
     res["dense_mha_decode_b1_h8_s512_d64"] = {"us_per_call": round(ms * 1e3, 2),
+                                               "us_per_call_prepared": round(ms_p * 1e3, 2),
                                                "algorithmic_bytes": 1_050_624}
     # the Llama-3-8B decode step through SDPA with dense (unpaged) K/V:
     # q [32, 32, 1, 128], k/v [32, 8, 4096, 128] (the q heads of a KV head
@@ -185,7 +189,10 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     k4 = torch.randn((1, HKV, 4096, D), generator=gg, device=dev).half()
     v4 = torch.randn((1, HKV, 4096, D), generator=gg, device=dev).half()
     ms = timed(lambda i: tsa.scaled_dot_product_attention(q4, k4, v4, enable_gqa=True), steps, warmup, stream)
-    res["dense_gqa_decode_b1_h32_8_s4096"] = {"us_per_call": round(ms * 1e3, 2), "kernels_per_step": 2}
+    call4 = tsa.SdpaCall(q4, k4, v4, enable_gqa=True)
+    ms_p = timed(lambda i: call4(), steps, warmup, stream)
+    res["dense_gqa_decode_b1_h32_8_s4096"] = {"us_per_call": round(ms * 1e3, 2),
+                                              "us_per_call_prepared": round(ms_p * 1e3, 2), "kernels_per_step": 2}
     del q4, k4, v4
     # long-context decode through SDPA with dense K/V: q [4, 64, 1, 128],
     # k/v [4, 8, 32768, 128] (keys split across blocks, partials merged)
@@ -371,9 +378,13 @@ def main():
         t = timed(lambda i: calls[i % nbuf](), args.steps, args.warmup, stream)
         relayout[name] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1),
                           "frac": round(rel_bytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-    # plain device copy of the same bytes, for reference
+    # plain device copies of the same bytes, for reference: torch's, and this
+    # library's flat nest (its vector kernel: 4 x 16 B per lane, loads before stores)
     t = timed(lambda i: outs_host[i % nbuf].copy_(xs[i % nbuf]), args.steps, args.warmup, stream)
     relayout["torch_copy_reference"] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1)}
+    flat = [DmaCopy(xs[i], outs_host[i], tsa.relayout.flat_plan(R * C)) for i in range(nbuf)]
+    t = timed(lambda i: flat[i % nbuf](), args.steps, args.warmup, stream)
+    relayout["flat_copy_reference"] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1)}
 
     result = {
         "metric": METRIC,

@@ -98,3 +98,26 @@ def test_relayout_graph_replays_match_oracle(cuda):
         got_t = tr.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
         assert np.array_equal(got_s, OR.to_sticks(bits).reshape(-1)), i
         assert np.array_equal(got_t, OR.transpose_restick(bits).reshape(-1)), i
+
+
+def test_dense_decode_graph_replays_match_eager(cuda):
+    """A prepared batch-1 dense decode (SdpaCall: 32 key splits + merge) in
+    a graph; q and the newest key/value row rewritten eagerly before each
+    replay; every replay bit-equal to the eager call."""
+    import torch_spyre_amd as tsa
+
+    gg = torch.Generator(device=cuda).manual_seed(SEED + 95)
+    q = torch.randn((1, 32, 1, 128), generator=gg, device=cuda).half()
+    k = torch.randn((1, 8, 4096, 128), generator=gg, device=cuda).half()
+    v = torch.randn((1, 8, 4096, 128), generator=gg, device=cuda).half()
+    call = tsa.SdpaCall(q, k, v, enable_gqa=True, return_lse=True)
+    g = _capture(cuda, call)
+    for i in range(3):
+        q.copy_(torch.randn(q.shape, generator=gg, device=cuda).half())
+        k[:, :, 4095].copy_(torch.randn((1, 8, 128), generator=gg, device=cuda).half())
+        v[:, :, 4095].copy_(torch.randn((1, 8, 128), generator=gg, device=cuda).half())
+        g.replay()
+        want, want_lse = tsa.scaled_dot_product_attention(q, k, v, enable_gqa=True, return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(call.out.view(torch.int16), want.view(torch.int16)), f"replay {i}"
+        assert torch.equal(call.lse, want_lse), f"replay {i}"

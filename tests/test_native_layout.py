@@ -189,7 +189,12 @@ def test_sdpa_call_workspace_routes(tsa):
 
     vt = L.spyre_sdpa_fwd_workspace_bytes(B, Hkv, 160, D)
     assert vt == B * Hkv * D * 192 * 2
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, Sq, 160, D) == 0
+    # no mask, a grid that fills the device (64 blocks x 8 >= 256 units): nothing
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 16, Hq, Hkv, Sq, 160, D) == 0
+    # no mask, a grid of at most an eighth of the device: a key split's partials, down to
+    # one 64-key step per block (batch-1 decode, 512 keys: 8 splits of [8 rows, 64 + 2] fp32)
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 512, 64) == 8 * 8 * 66 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 127, 64) == 0  # one step
     # staged as they lie: fp16 rows of 160 keys (320 B), bool rows of 160 B, broadcasts, wider rows
     assert need(1, [0, 0, 160, 1], 160) == 0
     assert need(3, [0, 0, 160, 1], 160) == 0

@@ -414,12 +414,15 @@ def test_workspace_only_for_masks(cuda):
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,Skv,D", [(1, 32, 8, 4096, 128), (1, 32, 8, 1500, 128), (1, 8, 8, 2048, 64),
-                                            (2, 64, 8, 3000, 128)])
+                                            (2, 64, 8, 3000, 128), (1, 8, 8, 512, 64), (1, 8, 8, 130, 64),
+                                            (1, 32, 8, 200, 128)])
 def test_key_split_for_small_grids(cuda, B, Hq, Hkv, Skv, D):
     """Decode with few (sequence, KV head) pairs: the keys are split across
     blocks so the grid fills the device, and the partials are merged (batch
     1 decode of the Llama-3-8B shape, a ragged last split, D 64 without
-    GQA, a key count that is no multiple of 64)."""
+    GQA, a key count that is no multiple of 64; grids of at most an eighth
+    of the device split down to one 64-key step per block: 512 keys in 8
+    splits, 130 keys as 64 + 64 + 2, 200 keys as 4 splits)."""
     from torch_spyre_amd import _lib
 
     assert _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, 1, Skv, D) > 0  # split
@@ -481,3 +484,76 @@ def test_bench_shape_prefill_sampled_heads(cuda, causal):
         first = out[0, :, 0].float()
         want = v[0, torch.arange(32) // 4, 0].float()
         assert torch.equal(first, want)
+
+
+PREPARED_CASES = [
+    # (B, Hq, Hkv, Sq, Skv, D, causal, mask kind)
+    (1, 8, 8, 1, 512, 64, False, None),       # batch-1 decode: 8 key splits of one step + merge
+    (1, 32, 8, 1, 4096, 128, False, None),    # Llama-3-8B batch-1 decode: 32 key splits + merge
+    (4, 32, 8, 1, 700, 128, False, None),     # packed GQA decode
+    (2, 8, 2, 100, 300, 128, True, None),     # causal prefill
+    (1, 4, 4, 64, 200, 64, False, "f16"),     # additive fp16 mask
+    (1, 4, 2, 50, 129, 128, False, "bool"),   # boolean keep-mask, GQA
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D,causal,mk", PREPARED_CASES, ids=str)
+def test_prepared_call_matches_eager(cuda, B, Hq, Hkv, Sq, Skv, D, causal, mk):
+    """SdpaCall, validated once and launched three times with q, k and v
+    rewritten in place before each launch: every launch bit-equal (out and
+    lse) to the eager call on the same inputs, and within the bar of the
+    oracle."""
+    import torch_spyre_amd as tsa
+
+    gg = torch.Generator(device=cuda).manual_seed(SEED + 300 + Skv)
+    q = torch.empty((B, Hq, Sq, D), dtype=torch.float16, device=cuda)
+    k = torch.empty((B, Hkv, Skv, D), dtype=torch.float16, device=cuda)
+    v = torch.empty((B, Hkv, Skv, D), dtype=torch.float16, device=cuda)
+    mask = None
+    if mk == "f16":
+        mask = torch.randn((Sq, Skv), generator=gg, device=cuda).half()
+    elif mk == "bool":
+        mask = torch.rand((B, 1, Sq, Skv), generator=gg, device=cuda) < 0.7
+        mask[..., 0] = True
+    call = tsa.SdpaCall(q, k, v, attn_mask=mask, is_causal=causal, enable_gqa=Hq != Hkv, return_lse=True)
+    for _ in range(3):
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=gg, device=cuda).half())
+        out, lse = call()
+        want, want_lse = tsa.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=causal,
+                                                          enable_gqa=Hq != Hkv, return_lse=True)
+        torch.cuda.synchronize()
+        assert out.shape == want.shape and out.stride() == want.stride()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+        assert torch.equal(lse, want_lse)
+    ref = OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), attn_mask=None if mask is None else mask.cpu(),
+                           is_causal=causal)
+    assert_close(out, ref)
+
+
+def test_prepared_call_refuses_copies(cuda):
+    """Operands the kernel cannot read as they lie are copied by the eager
+    call but refused by SdpaCall, which must read the caller's storage on
+    every launch."""
+    import torch_spyre_amd as tsa
+
+    q = randn((1, 8, 1, 64), SEED + 320).to(cuda)
+    kp = randn((1, 8, 512, 65), SEED + 321).to(cuda)
+    k = kp[..., :64]  # row stride 65: not a multiple of 8
+    v = randn((1, 8, 512, 64), SEED + 322).to(cuda)
+    with pytest.raises(ValueError):
+        tsa.SdpaCall(q, k, v)
+    assert_close(tsa.scaled_dot_product_attention(q, k, v), OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu()))
+
+
+def test_stream_pointer_follows_current_stream(cuda):
+    """The launch stream is the device's current stream, inside a stream
+    context too."""
+    from torch_spyre_amd.relayout import _stream_ptr
+
+    assert _stream_ptr(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    s = torch.cuda.Stream(device=cuda)
+    with torch.cuda.stream(s):
+        assert _stream_ptr(cuda) == s.cuda_stream
+        assert _stream_ptr(torch.device("cuda")) == s.cuda_stream
+    assert _stream_ptr(cuda) == torch.cuda.current_stream(cuda).cuda_stream

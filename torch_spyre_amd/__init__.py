@@ -52,6 +52,7 @@ from .attention import (  # noqa: E402
     workspace_bytes,
 )
 from .sdpa import (  # noqa: E402
+    SdpaCall,
     Unsupported,
     scaled_dot_product_attention,
     sdpa_override,
@@ -67,5 +68,5 @@ __all__ = [
     "PagedDecode", "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
     "paged_decode_merge", "paged_decode_split",
     "sdpa_decode", "v_page_layout", "workspace_bytes",
-    "Unsupported", "scaled_dot_product_attention", "sdpa_override", "sdpa_overrideable",
+    "SdpaCall", "Unsupported", "scaled_dot_product_attention", "sdpa_override", "sdpa_overrideable",
 ]

@@ -24,7 +24,11 @@ from .layout import SpyreTensorLayout, dma_plan, get_device_dtype, restick_plan
 
 
 def _stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of the device's current stream (what
+    ``torch.cuda.current_stream(device).cuda_stream`` returns, without
+    building the Stream object: ~0.2 against ~1.9 µs per call)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def _require_cuda(t: torch.Tensor, name: str) -> None:
@@ -153,6 +157,14 @@ def d2h_buffer(buf: torch.Tensor, layout: SpyreTensorLayout, size: Sequence[int]
     return out
 
 
+def flat_plan(n: int) -> list:
+    """The DMA nest of a contiguous copy of n elements."""
+    info = _lib.StrideInfo()
+    info.rank = 1
+    info.size[0], info.stride_src[0], info.stride_dst[0] = n, 1, 1
+    return [info]
+
+
 def copy_buffer(src: torch.Tensor, dst: torch.Tensor) -> None:
     """dst <- src byte for byte (same allocation size): one flat DMA nest."""
     if src.untyped_storage().nbytes() != dst.untyped_storage().nbytes() or src.dtype != dst.dtype:
@@ -160,10 +172,7 @@ def copy_buffer(src: torch.Tensor, dst: torch.Tensor) -> None:
     n = src.untyped_storage().nbytes() // src.element_size()
     if n == 0:
         return
-    info = _lib.StrideInfo()
-    info.rank = 1
-    info.size[0], info.stride_src[0], info.stride_dst[0] = n, 1, 1
-    dma_copy(src, dst, [info])
+    dma_copy(src, dst, flat_plan(n))
 
 
 def relayout_into(src: torch.Tensor, dst: torch.Tensor, host_size: Sequence[int], host_stride: Sequence[int],

@@ -24,6 +24,7 @@ of the reference's plain softmax.  All work runs in the HIP kernels of
 from __future__ import annotations
 
 import math
+from collections import OrderedDict
 from typing import Optional
 
 import torch
@@ -44,34 +45,74 @@ def workspace_bytes(B: int, Hkv: int, Skv: int, D: int) -> int:
     return int(_lib.lib().spyre_sdpa_fwd_workspace_bytes(B, Hkv, Skv, D))
 
 
-def _operand(t: torch.Tensor, name: str) -> torch.Tensor:
-    """fp16 CUDA [B, H, S, D] whose rows the kernel can read as 16-byte
-    vectors (feature stride 1, other strides multiples of 8, 16-byte
-    aligned); anything else is copied into that form first."""
-    _require_cuda(t, name)
+def _kernel_ready(t: torch.Tensor) -> bool:
+    """Rows the kernel can read as 16-byte vectors: feature stride 1, other
+    strides multiples of 8, 16-byte aligned."""
+    st = t.stride()
+    return st[3] == 1 and st[0] % 8 == 0 and st[1] % 8 == 0 and st[2] % 8 == 0 and t.data_ptr() % 16 == 0
+
+
+def _operand(t: torch.Tensor, name: str, copy: bool = True) -> torch.Tensor:
+    """fp16 CUDA [B, H, S, D] in kernel form; anything else is copied into
+    that form first (copy=False: refused instead)."""
+    if not t.is_cuda:
+        _require_cuda(t, name)
     if t.dim() != 4:
         raise ValueError(f"{name} must be 4-D [B, H, S, D]")
     if t.dtype != torch.float16:
         raise TypeError(f"{name} must be float16 (got {t.dtype})")
-    ok = t.stride(3) == 1 and all(t.stride(i) % 8 == 0 for i in range(3)) and t.data_ptr() % 16 == 0
+    if _kernel_ready(t):
+        return t
+    if not copy:
+        raise ValueError(f"{name} needs feature stride 1, other strides multiples of 8 and 16-byte alignment")
     # contiguous() would hand back a tensor torch already counts as
     # contiguous (odd strides on size-1 dims, an unaligned storage offset)
-    return t if ok else t.clone(memory_format=torch.contiguous_format)
+    return t.clone(memory_format=torch.contiguous_format)
 
 
-def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                                 attn_mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
-                                 is_causal: bool = False, scale: Optional[float] = None,
-                                 enable_gqa: bool = False, return_lse: bool = False,
-                                 workspace: Optional[torch.Tensor] = None):
-    """``F.scaled_dot_product_attention`` on fp16 CUDA tensors: query
-    [B, Hq, Sq, D], key/value [B, Hkv, Skv, D], D in {64, 128}."""
-    q = _operand(query, "query")
-    k = _operand(key, "key")
-    v = _operand(value, "value")
+# What a call needs that depends only on its geometry -- the stride arrays
+# handed to the library and the workspace size -- kept per geometry, so a
+# repeated call builds neither again.
+_PLANS: "OrderedDict[tuple, tuple]" = OrderedDict()
+_PLANS_MAX = 256
+
+
+def _geometry_plan(q, k, v, mask, kind: int, is_causal: bool):
+    key = (q.shape, q.stride(), k.shape, k.stride(), v.stride(), kind, bool(is_causal), q.device.index,
+           None if mask is None else (mask.stride(), mask.data_ptr() % 16))
+    plan = _PLANS.get(key)
+    if plan is not None:
+        _PLANS.move_to_end(key)
+        return plan
+    B, Hq, Sq, D = q.shape
+    _, Hkv, Skv, _ = k.shape
+    mstrides = _lib.i64_array(mask.stride()) if mask is not None else None
+    # The call's workspace: without a mask, a key split's partials when the
+    # blocks would not fill the device (none for causal calls); none for
+    # masks the kernel stages as they lie, a copy with 16-byte rows for other
+    # fp16 / bool masks, V's relayout for fp32 masks.
+    need = 0
+    if kind != MASK_NONE or not is_causal:
+        need = int(_lib.lib().spyre_sdpa_fwd_call_workspace_bytes(
+            mask.data_ptr() if mask is not None else None, kind, mstrides, B, Hq, Hkv, Sq, Skv, D))
+    plan = (_lib.i64_array(q.stride()[:3]), _lib.i64_array(k.stride()[:3]), _lib.i64_array(v.stride()[:3]),
+            mstrides, need)
+    _PLANS[key] = plan
+    if len(_PLANS) > _PLANS_MAX:
+        _PLANS.popitem(last=False)
+    return plan
+
+
+def _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa, return_lse, workspace,
+             copy_operands: bool):
+    """Validates a call and allocates its output: (library arguments less
+    the stream, output view, lse, tensors the arguments point into)."""
+    q = _operand(query, "query", copy_operands)
+    k = _operand(key, "key", copy_operands)
+    v = _operand(value, "value", copy_operands)
     B, Hq, Sq, D = q.shape
     Bk, Hkv, Skv, Dk = k.shape
-    if tuple(v.shape) != (Bk, Hkv, Skv, Dk) or Bk != B or Dk != D:
+    if v.shape != k.shape or Bk != B or Dk != D:
         raise ValueError("key/value must be [B, Hkv, Skv, D] matching query")
     if Hq != Hkv and not enable_gqa:
         raise ValueError("Hq != Hkv requires enable_gqa=True")
@@ -81,7 +122,7 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
         raise Unsupported("Attention dropout not implemented")
     if is_causal and attn_mask is not None:
         raise ValueError("is_causal and attn_mask are exclusive")
-    kind, mask, mstrides = MASK_NONE, None, None
+    kind, mask = MASK_NONE, None
     if attn_mask is not None:
         m = torch.as_tensor(attn_mask, device=q.device)
         if m.dtype not in _MASK_KIND:
@@ -90,18 +131,10 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
         mask = m.expand(B, Hq, Sq, Skv)
         if mask.dtype == torch.bool:
             mask = mask.view(torch.uint8)
-        mstrides = _lib.i64_array(mask.stride())
+    qs, ks, vs, mstrides, need = _geometry_plan(q, k, v, mask, kind, is_causal)
     s = 1.0 / math.sqrt(D) if scale is None else float(scale)
     out = torch.empty((B, Sq, Hq, D), dtype=torch.float16, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
-    # The call's workspace: without a mask, a key split's partials when the
-    # blocks would not fill the device (none for causal calls); none for
-    # masks the kernel stages as they lie, a copy with 16-byte rows for other
-    # fp16 / bool masks, V's relayout for fp32 masks.
-    need = 0
-    if kind != MASK_NONE or not is_causal:
-        need = int(_lib.lib().spyre_sdpa_fwd_call_workspace_bytes(
-            mask.data_ptr() if mask is not None else None, kind, mstrides, B, Hq, Hkv, Sq, Skv, D))
     if workspace is None and need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     elif workspace is not None and need and kind != MASK_NONE:
@@ -111,15 +144,49 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
             raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, need {floor}")
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    rc = _lib.lib().spyre_sdpa_fwd_f16(
-        q.data_ptr(), _lib.i64_array(q.stride()[:3]), k.data_ptr(), _lib.i64_array(k.stride()[:3]),
-        v.data_ptr(), _lib.i64_array(v.stride()[:3]), mask.data_ptr() if mask is not None else None,
-        kind, mstrides, int(bool(is_causal)), s, out.data_ptr(),
-        lse.data_ptr() if lse is not None else None, ws_ptr, ws_bytes, B, Hq, Hkv, Sq, Skv, D,
-        _stream_ptr(q.device))
-    _lib.check("spyre_sdpa_fwd_f16", rc)
-    out = out.transpose(1, 2)
+    args = (q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, mask.data_ptr() if mask is not None else None,
+            kind, mstrides, int(bool(is_causal)), s, out.data_ptr(), lse.data_ptr() if lse is not None else None,
+            ws_ptr, ws_bytes, B, Hq, Hkv, Sq, Skv, D)
+    return args, out.transpose(1, 2), lse, (q, k, v, mask, workspace)
+
+
+def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                 attn_mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                                 is_causal: bool = False, scale: Optional[float] = None,
+                                 enable_gqa: bool = False, return_lse: bool = False,
+                                 workspace: Optional[torch.Tensor] = None):
+    """``F.scaled_dot_product_attention`` on fp16 CUDA tensors: query
+    [B, Hq, Sq, D], key/value [B, Hkv, Skv, D], D in {64, 128}."""
+    args, out, lse, _ = _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa,
+                                 return_lse, workspace, True)
+    _lib.check("spyre_sdpa_fwd_f16", _lib.lib().spyre_sdpa_fwd_f16(*args, _stream_ptr(query.device)))
     return (out, lse) if return_lse else out
+
+
+class SdpaCall:
+    """A validated ``scaled_dot_product_attention`` that can be launched
+    repeatedly, the dense counterpart of ``PagedDecode``: shapes, strides,
+    the workspace and the output are settled once, and each call only passes
+    the stored pointers to the library.  The operands must already be in
+    kernel form (feature stride 1, other strides multiples of 8, 16-byte
+    aligned; no copy is made) and must stay alive with their storage; the
+    caller may rewrite their contents between calls.  Every call writes the
+    same ``out`` (and ``lse``), on the stream current at that moment, so the
+    calls can be captured into a HIP graph (the library allocates and clears
+    nothing)."""
+
+    def __init__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                 attn_mask: Optional[torch.Tensor] = None, is_causal: bool = False, scale: Optional[float] = None,
+                 enable_gqa: bool = False, return_lse: bool = False, workspace: Optional[torch.Tensor] = None):
+        self._args, self.out, self.lse, self._keep = _prepare(query, key, value, attn_mask, 0.0, is_causal,
+                                                              scale, enable_gqa, return_lse, workspace, False)
+        self._fn = _lib.lib().spyre_sdpa_fwd_f16
+        self._device = query.device
+        self._return_lse = return_lse
+
+    def __call__(self):
+        _lib.check("spyre_sdpa_fwd_f16", self._fn(*self._args, _stream_ptr(self._device)))
+        return (self.out, self.lse) if self._return_lse else self.out
 
 
 def sdpa_overrideable(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
