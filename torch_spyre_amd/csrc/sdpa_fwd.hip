@@ -710,6 +710,43 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         psum = __builtin_amdgcn_fdot2(f16x2{pb[j][2 * e], pb[j][2 * e + 1]}, f16x2{1, 1}, psum, false);
     l_run += psum;
   };
+  // P (fp16) of S^T registers 8j .. 8j + 7 of a half: the B operand of the
+  // half's PV k-step j.  Returns the sum of the same fp16 values.
+  auto softmax_q = [&](const f32x16& s, int j, float neg_m, f16x8& pb) -> float {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int rr = 8 * j + e;
+      pb[e] = static_cast<_Float16>(fast_exp2(PRESCALED ? s[rr] : __builtin_fmaf(s[rr], scale_abs, neg_m)));
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      psum = __builtin_amdgcn_fdot2(f16x2{pb[2 * e], pb[2 * e + 1]}, f16x2{1, 1}, psum, false);
+    return psum;
+  };
+  // A move of the running max to m_new = max(m_run, mx): O and l rescaled;
+  // PRESCALED: S(t) and S(t+1) shifted with m_use, and the -m tile.
+  auto rescale = [&](f32x16 (&s)[2], f32x16 (&ahead)[2], float mx) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int dm = 0; dm < DM; ++dm) o[dm] *= alpha;
+    m_run = m_new;
+    if constexpr (PRESCALED) {
+      const float m_use_new = m_new == -INFINITY ? m_use : m_new;  // lanes still without a score keep 0
+      const float d = m_use_new - m_use;
+      m_use = m_use_new;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        s[0][rr] -= d;
+        s[1][rr] -= d;
+        ahead[0][rr] -= d;
+        ahead[1][rr] -= d;
+        neg_m_tile[rr] = -m_use;
+      }
+    }
+  };
   // The 2 DK + 4 DM MFMAs of a step in issue order, each with its LDS operand
   // fragment: 0 .. 2DK-1 the K operands of S(t+1) (half i / DK, k-step
   // i % DK), then the V^T operands of O^T += V^T P^T (two transposed reads
@@ -728,9 +765,9 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
                                                   16 * ((lane >> 4) & 1) + 4 * (lane & 3));
   auto tr4 = [&](uint32_t e) { return tr_read4(lds + e); };
   auto frag = [&](const _Float16* k1, int i) -> f16x8 {
-    if (i < 2 * DK)
-      return *reinterpret_cast<const f16x8*>(k1 + ((i / DK) * 32 + key32_of(col)) * L::kRowK + 8 * half +
-                                             16 * (i % DK));
+    if (i < 2 * DK)  // the two halves' chains alternate: half i % 2, k-step i / 2
+      return *reinterpret_cast<const f16x8*>(k1 + ((i % 2) * 32 + key32_of(col)) * L::kRowK + 8 * half +
+                                             16 * (i / 2));
     i -= 2 * DK;
     // keys 16 (i / DM) + 8 half .. + 7 of feature 32 (i % DM) + col
     const uint32_t e = vtr + (16 * (i / DM)) * L::kRowV + 32 * (i % DM);
@@ -749,6 +786,28 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read (K)
       else if (f < kNF)
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two (V, transposed)
+    }
+  };
+
+  // Interleaves MFMAs i0 .. i1 - 1 with the rest of their region: after
+  // each MFMA the reads of the fragment kPrefetch ahead, then te (after the
+  // region's even MFMAs) or to (odd) transcendental and nv other VALU
+  // instructions.
+  auto interleave_mix = [](int i0, int i1, int te, int to, int nv) {
+    for (int i = i0; i < i1; ++i) {
+      const int f = i + kPrefetch;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      if (f < 2 * DK)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read (K)
+      else if (f < kNF)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two (V, transposed)
+      const int nt = (i - i0) % 2 == 0 ? te : to;
+      if (nt == 1) __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // transcendental
+      if (nt == 2) __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
+      if (nv == 1) __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // other VALU
+      if (nv == 2) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      if (nv == 3) __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      if (nv == 4) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
     }
   };
 
@@ -882,30 +941,44 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       };
       if constexpr (MK == kNoMask) {
         if (edge(t)) mask_step(t, cur);
+        // Region A: the 2 DK MFMAs of S(t+1) beside P(t), computed against
+        // the running max as it stands.  The max matters only as a bound:
+        // while every lane's sum of P(t) stays <= 2^8, so does every P, and
+        // nothing moves.  Otherwise (and at a wavefront's first scores) the
+        // branch below takes the row max, rescales and redoes P(t) -- so the
+        // common step computes no max at all.
         nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < DK; ++ks) mfma(ks, qv[ks], nxt[0]);
-        interleave_reads(0, DK);
-        update_max(cur, nxt[0], nullptr, row_max(cur));
-        const float neg_m = m_run == -INFINITY ? 0.f : -m_run;
-        f16x8 p0[2], p1[2];
         nxt[1] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < DK; ++ks) mfma(DK + ks, qv[ks], nxt[1]);
-        softmax_half(cur[0], neg_m, p0);
-        interleave_reads(DK, 2 * DK);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int ks = 0; ks < DK; ++ks) {
+          mfma(2 * ks, qv[ks], nxt[0]);
+          mfma(2 * ks + 1, qv[ks], nxt[1]);
+        }
+        f16x8 p0[2], p1[2];
+        float neg_m = m_run == -INFINITY ? 0.f : -m_run;
+        float ps = softmax_q(cur[0], 0, neg_m, p0[0]) + softmax_q(cur[0], 1, neg_m, p0[1]) +
+                   softmax_q(cur[1], 0, neg_m, p1[0]) + softmax_q(cur[1], 1, neg_m, p1[1]);
+        // Before the branch: otherwise the compiler moves P(t) into its
+        // fall-through path, after region A.
+        asm volatile("" : "+v"(p0[0]), "+v"(p0[1]), "+v"(p1[0]), "+v"(p1[1]), "+v"(ps));
+        interleave_mix(0, 2 * DK, 2, 2, 2);
+        if (__builtin_amdgcn_ballot_w64(!(ps <= 256.f) || m_run == -INFINITY) != 0) {
+          rescale(cur, nxt, row_max(cur));
+          neg_m = m_run == -INFINITY ? 0.f : -m_run;
+          ps = softmax_q(cur[0], 0, neg_m, p0[0]) + softmax_q(cur[0], 1, neg_m, p0[1]) +
+               softmax_q(cur[1], 0, neg_m, p1[0]) + softmax_q(cur[1], 1, neg_m, p1[1]);
+        }
+        l_run += ps;
+        // Region B: O^T += V^T P^T.
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
-        softmax_half(cur[1], neg_m, p1);
-        interleave_reads(2 * DK, 2 * DK + 2 * DM);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + 2 * DM + j * DM + dm, p1[j], o[dm]);
+        interleave_reads(2 * DK, kNF);
       } else {
         // A mask can leave a step nothing to add: every score of the
         // wavefront's block -inf or more than 32 below its row's running
@@ -915,11 +988,12 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
         if (edge(t)) mask_step(t, cur);
         const float mx = row_max(cur);
         const bool live = __builtin_amdgcn_ballot_w64(mx > -INFINITY && mx >= m_run - 32.f) != 0;
+        nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
+        nxt[1] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          nxt[h2] = PRESCALED ? neg_m_tile : f32x16{};
-#pragma unroll
-          for (int ks = 0; ks < DK; ++ks) mfma(h2 * DK + ks, qv[ks], nxt[h2]);
+        for (int ks = 0; ks < DK; ++ks) {
+          mfma(2 * ks, qv[ks], nxt[0]);
+          mfma(2 * ks + 1, qv[ks], nxt[1]);
         }
         interleave_reads(0, 2 * DK);
         if (live) {
