@@ -302,3 +302,96 @@ def test_empty_and_errors(cuda):
         tsa.relayout.dma_copy(src, dst, [info])
     with pytest.raises(RuntimeError):  # CPU buffers: no CPU path
         tsa.relayout.h2d_buffer(torch.zeros(64, 64, dtype=torch.float16), stl)
+
+
+# Whole-tile nests for the stepped kernels: 1 to 4 tile loops, lengths that
+# are powers of two and lengths that are not.  (sizes, padded length of dim
+# 1 of the host buffer the tensor is a view of, or None for a contiguous
+# tensor: the padding keeps the two leading loops from merging.)
+#   [64, 2048]        to sticks: A tiles 2               from: B tiles 2 (32 x 32)
+#   [96, 4096]        to: B tiles 2, A tiles 3            from: B tiles 6 (64 x 16)
+#   [3, 64, 4096]     to: B 2, A 2, outer 3               from: B 4, outer 3
+#   [3, 5, 64, 4096]  to: B 2, A 2, outer 5, outer 3      from: B 4, outer 5, 3
+# Row-major <-> default sticks through the stepped stick-tile kernel.  The
+# stick loop (host dim 0 in the default layout) and the last dim's sticks
+# form the tiles; the remaining loops step whole tiles.  Loops that are
+# dense on both sides merge (the B tiles with the next host dim when host
+# rows are dense), so [96, 3, 16, 4096] steps two loops and the view
+# [96, 3, 8, 4096] of a [96, 3, 8, 4160] buffer three; in the view of a
+# [96, 3, 10, 4160] buffer nothing merges: four.
+STICK_STEP_CASES = [([64, 2048], None), ([96, 4096], None), ([96, 3, 16, 4096], None),
+                    ([96, 3, 8, 4096], {3: 4160}), ([96, 3, 8, 4096], {2: 10, 3: 4160})]
+
+
+def _host_view(sizes, pad, seed, cuda):
+    """Random bit patterns as a CUDA tensor of `sizes`: contiguous, or with
+    pad = {dim: n, ...} the view [..., :sizes[dim], ...] of a buffer whose
+    dims are n long.  Returns the tensor, the flat store, its strides and
+    offset."""
+    pad = pad or {}
+    full = [pad.get(d, s) for d, s in enumerate(sizes)]
+    store = OR.random_finite_f16_bits((int(np.prod(full)),), seed)
+    x = _bits_tensor(store, cuda).view(full)
+    for d in pad:
+        x = x.narrow(d, 0, sizes[d])
+    return x, store, list(x.stride()), x.storage_offset()
+
+
+@pytest.mark.parametrize("sizes,pad", STICK_STEP_CASES, ids=str)
+def test_stepped_stick_tiles_vs_oracle(cuda, sizes, pad):
+    """Host order (contiguous or a strided view) -> default sticks -> host
+    order: device bytes equal the oracle's H2D, and D2H restores every
+    element.  The layout's stride_map refers to the host tensor's own
+    strides, as x.to(device_layout=...) records them."""
+    import torch_spyre_amd as tsa
+
+    x, store, strides, off = _host_view(sizes, pad, SEED + 400 + sum(sizes) + len(pad or {}), cuda)
+    order = list(range(len(sizes)))
+    stl = tsa.SpyreTensorLayout(list(sizes), strides, torch.float16, order)
+    dev = tsa.to_device_layout(x, stl)
+    want = OL.h2d(store, list(sizes), strides, off, OL.stl_init(list(sizes), strides, "float16", order))
+    assert np.array_equal(_as_bits(dev).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    torch.cuda.synchronize()
+    assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))
+
+
+# Transposes (the stick moves from the last dim to the one before it):
+# device restickify of 64 x 64-element tiles, four consecutive ones to a
+# wavefront, so the first stepped loop's count is a multiple of 4:
+# [768, 1024] and [4, 512, 256] step both ways; in [768, 640] one
+# direction's first loop has 10 tiles, in [3, 256, 320] both directions'
+# is dim 0 (3), and those take the LDS-staged transpose.  The host view
+# [3, 5, 128, 256] of a [3, 6, 128, 256] buffer goes straight to transposed
+# sticks (tile loops 4, 2, then 5 and 3) and back.
+@pytest.mark.parametrize("sizes", [[768, 640], [768, 1024], [3, 256, 320], [4, 512, 256]], ids=str)
+def test_stepped_restickify_vs_oracle(cuda, sizes):
+    import torch_spyre_amd as tsa
+
+    order = list(range(len(sizes)))
+    order[-2], order[-1] = order[-1], order[-2]
+    strides = OL.contiguous_strides(sizes)
+    src = tsa.SpyreTensorLayout(sizes, torch.float16)
+    dst = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + 410 + sum(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    out = tsa.restickify(tsa.to_device_layout(x, src), dst)
+    want = OL.h2d(bits, sizes, strides, 0, OL.stl_init(sizes, strides, "float16", order))
+    assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
+    back = tsa.restickify(out, src)
+    assert np.array_equal(_as_bits(back).reshape(-1), _as_bits(tsa.to_device_layout(x, src)).reshape(-1))
+
+
+def test_stepped_transpose_from_strided_host_vs_oracle(cuda):
+    import torch_spyre_amd as tsa
+
+    sizes = [3, 5, 128, 256]
+    x, store, strides, off = _host_view(sizes, {1: 6}, SEED + 420, cuda)
+    order = [0, 1, 3, 2]
+    dst = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    dev = tsa.to_device_layout(x, dst)
+    want = OL.h2d(store, sizes, strides, off, OL.stl_init(sizes, strides, "float16", order))
+    assert np.array_equal(_as_bits(dev).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    torch.cuda.synchronize()
+    assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))
