@@ -19,7 +19,8 @@ and long-context (q [4, 64, 1, 128], k/v [4, 8, 32768, 128]) counterparts, the r
 ~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
 heads, append one token at position 131072, attend over 131073 tokens) and
 prefill SDPA, causal, full and with an fp16 / boolean [4096, 4096] mask
-(batch 1, 32 q / 8 KV heads, 4096 tokens);
+(batch 1, 32 q / 8 KV heads, 4096 tokens), and for reference torch's fp16
+[8192, 8192] GEMM (the MFMA rate a plain library GEMM reaches on the box);
 under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
 transpose-restick, rotating 9 buffer pairs (576 MiB), with torch's CPU
 view/permute/contiguous of the same closed forms as its CPU baseline.
@@ -289,6 +290,18 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
             "us_per_step": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
             "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / PEAK_F16, 4), "flops": flops,
             "kernels_per_step": 1}
+    del masks, ws
+    # For reference, the MFMA rate a plain library GEMM reaches on the same
+    # box: torch's fp16 [8192, 8192] x [8192, 8192] (hipBLASLt), timed the
+    # same way after the same warm-up.
+    n = 8192
+    ga = torch.randn((n, n), generator=gg, device=dev).half()
+    gb = torch.randn((n, n), generator=gg, device=dev).half()
+    ms = timed(lambda i: torch.mm(ga, gb), max(steps // 5, 10), PREFILL_WARMUP, stream)
+    flops = 2 * n ** 3
+    res["torch_gemm_f16_8192_reference"] = {
+        "us_per_step": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+        "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / PEAK_F16, 4), "flops": flops}
     return res
 
 
