@@ -191,10 +191,17 @@ def test_sdpa_call_workspace_routes(tsa):
     assert vt == B * Hkv * D * 192 * 2
     # no mask, a grid that fills the device (64 blocks x 8 >= 256 units): nothing
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 16, Hq, Hkv, Sq, 160, D) == 0
-    # no mask, a grid of at most an eighth of the device: a key split's partials, down to
-    # one 64-key step per block (batch-1 decode, 512 keys: 8 splits of [8 rows, 64 + 2] fp32)
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 512, 64) == 8 * 8 * 66 * 4
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 127, 64) == 0  # one step
+    # no mask, one row tile (g q heads x Sq <= 32 rows): the short-decode kernel takes up to
+    # 8 x 64 keys per block at D 64 (batch-1 decode, 512 keys: one block per head, no
+    # partials) and 8 x 32 at D 128; longer runs split into such blocks while they fit one
+    # round of the device: 4096 keys at D 128 -> 16 splits of [32 rows, 128 + 2] fp32
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 512, 64) == 0
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 513, 64) == 8 * 2 * 66 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 4096, 128) == 32 * 16 * 130 * 4
+    # 64 splits of 8 (sequence, KV head) blocks pass one round: the split of the LDS kernel
+    # (a grid of at most an eighth of the device splits down to one 64-key step per block)
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 16384, 128) == 32 * 32 * 130 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 40, 127, 64) == 0  # one step
     # staged as they lie: fp16 rows of 160 keys (320 B), bool rows of 160 B, broadcasts, wider rows
     assert need(1, [0, 0, 160, 1], 160) == 0
     assert need(3, [0, 0, 160, 1], 160) == 0

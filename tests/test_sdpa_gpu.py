@@ -413,25 +413,52 @@ def test_workspace_only_for_masks(cuda):
                                          workspace=torch.empty(16, dtype=torch.uint8, device=cuda))
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,Skv,D", [(1, 32, 8, 4096, 128), (1, 32, 8, 1500, 128), (1, 8, 8, 2048, 64),
-                                            (2, 64, 8, 3000, 128), (1, 8, 8, 512, 64), (1, 8, 8, 130, 64),
-                                            (1, 32, 8, 200, 128)])
-def test_key_split_for_small_grids(cuda, B, Hq, Hkv, Skv, D):
-    """Decode with few (sequence, KV head) pairs: the keys are split across
-    blocks so the grid fills the device, and the partials are merged (batch
-    1 decode of the Llama-3-8B shape, a ragged last split, D 64 without
-    GQA, a key count that is no multiple of 64; grids of at most an eighth
-    of the device split down to one 64-key step per block: 512 keys in 8
-    splits, 130 keys as 64 + 64 + 2, 200 keys as 4 splits)."""
+# Decode with few (sequence, KV head) pairs.  One row tile (g q heads x
+# Sq <= 32 rows) runs the short-decode kernel: a block takes 8 wavefront
+# slices of 64 keys (D 64) or 32 (D 128), all loaded at once, and longer key
+# runs split into such blocks while they all fit one round of the device
+# (the Llama-3-8B batch-1 step: 16 splits of 256 keys; a ragged last split;
+# D 64 without GQA); 512 keys at D 64 and 200 at D 128 are one block (a
+# ragged last slice), 130 keys leave 5 slices empty.  Past one round, the
+# LDS kernel splits instead (16384 keys: 32 splits of 512; 20000: 32 of
+# 640, the last 160).  split: whether the call needs partials.
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,D,split", [(1, 32, 8, 4096, 128, True), (1, 32, 8, 1500, 128, True),
+                                                  (1, 8, 8, 2048, 64, True), (2, 64, 8, 3000, 128, True),
+                                                  (1, 8, 8, 512, 64, False), (1, 8, 8, 130, 64, False),
+                                                  (1, 32, 8, 200, 128, False), (1, 32, 8, 16384, 128, True),
+                                                  (1, 8, 8, 20000, 64, True)])
+def test_key_split_for_small_grids(cuda, B, Hq, Hkv, Skv, D, split):
     from torch_spyre_amd import _lib
 
-    assert _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, 1, Skv, D) > 0  # split
+    assert (_lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, 1, Skv, D) > 0) == split
     q = randn((B, Hq, 1, D), SEED + 60 + Skv)
     k, v = randn((B, Hkv, Skv, D), SEED + 61), randn((B, Hkv, Skv, D), SEED + 62)
     out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
     assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
     _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
     assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
+# The short-decode kernel with several query rows per q head (Sq x g <= 32:
+# speculative decode, a short chunk), an explicit scale outside the
+# prescaled range (|scale log2 e| > 1) and a negative one, empty contexts,
+# and q / k / v views with padded strides.
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D,scale", [(2, 8, 2, 4, 700, 64, None), (1, 16, 2, 3, 300, 128, None),
+                                                     (3, 4, 4, 32, 100, 128, None), (1, 8, 8, 1, 512, 64, 2.0),
+                                                     (2, 32, 8, 1, 260, 128, -0.3), (1, 8, 8, 5, 0, 64, None)])
+def test_short_decode_rows_and_scales(cuda, B, Hq, Hkv, Sq, Skv, D, scale):
+    q = randn((B, Hq, Sq, D + 8), SEED + 70 + Skv)[..., :D]
+    k = randn((B, Hkv, Skv, D + 16), SEED + 71)[..., :D]
+    v = randn((B, Hkv, Skv, D), SEED + 72)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True, scale=scale)
+    if Skv == 0:
+        assert torch.equal(out.cpu(), torch.zeros_like(out.cpu()))
+        assert bool(torch.isneginf(lse.cpu()).all())
+        return
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, scale=scale))
+    if scale is None or scale > 0:  # the fp64 decomposition splits the scale as sqrt(scale) on q and k
+        _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, scale=scale, return_lse=True)
+        assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
 
 
 def test_argument_errors(cuda):

@@ -1121,6 +1121,222 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     a.lse[(static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi] = l > 0.f ? (m_run + log2f(l)) * kLn2 : -INFINITY;
 }
 
+// ---- 4. short decode: a block's keys all in flight at once ----------------
+//
+// Calls without a mask or causal flag whose block holds one row tile (the g
+// q heads of a KV head times Sq <= 32 rows) and at most kWaves2 * KW keys
+// (KW = 64 keys at D = 64, 32 at D = 128): wavefront w loads keys
+// kb + w KW .. + KW - 1 of K and V into its own LDS slice, all loads issued
+// at kernel start, and computes its partial of the rows over them (S^T =
+// K Q^T, softmax, O^T = V^T P^T as in sdpa_fwd_lds_kernel, the V^T operands
+// through transposing LDS reads).  The 8 partials are then folded in LDS:
+// the call is one round of loads and one kernel.  Longer key runs are split
+// across blocks as in sdpa_fwd_lds_kernel (partials to the workspace, then
+// sdpa_split_merge_kernel).
+template <int D>
+struct ShortLds {
+  static constexpr int kKW = D == 64 ? 64 : 32;          // keys per wavefront
+  static constexpr int kRowK = D + kPadH;                // K row, halves (padded)
+  static constexpr int kUK = kRowK / 8;                  // 16-byte units per K row
+  static constexpr int kNK = (kKW * kUK + 63) / 64;      // loads per K slice
+  static constexpr int kNV = kKW * D / 8 / 64;           // loads per V slice (rows of D halves)
+  static constexpr int kSliceB = (kNK + kNV) * 1024;     // bytes per wavefront
+  static constexpr int kFoldF = D / 2 + 2;               // per-lane floats of a partial: O^T, m, l
+  static constexpr int kBytes = kWaves2 * kSliceB;
+  static_assert(kKW * D / 8 % 64 == 0, "V slices must be whole loads");
+  static_assert(kWaves2 * 64 * kFoldF * 4 <= kBytes, "the fold reuses the slices");
+};
+
+template <int D, bool PRESCALED>
+__global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a) {
+  using L = ShortLds<D>;
+  constexpr int DK = D / 16, DM = D / 32;
+  constexpr int KW = L::kKW, MT = KW / 32;  // 32-key S^T tiles per wavefront
+  __shared__ __align__(16) _Float16 lds[L::kBytes / 2];
+
+  // item = ((b * Hkv + kvh) * gp + gi) * nsplit + sp (one query block).
+  uint32_t item = blockIdx.x;
+  if (a.xcd_remap) item = (item % 8) * (a.n_items / 8) + item / 8;
+  const int sp = static_cast<int>(item % a.nsplit);
+  item /= a.nsplit;
+  const int gi = static_cast<int>(item % a.gp);
+  const uint32_t r = item / a.gp;
+  const int kvh = static_cast<int>(r % a.Hkv);
+  const int b = static_cast<int>(r / a.Hkv);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  __builtin_assume(wave >= 0 && wave < kWaves2);
+  const int col = lane & 31, half = lane >> 5;
+  const int pack = a.pack;
+  const int qi = col / pack;  // this lane's row: query qi, q head h
+  const int h = kvh * a.g + gi * pack + (col - qi * pack);
+  const bool q_ok = qi < a.Sq;
+
+  // This wavefront's keys: kw .. kw + KW - 1, those below key_end visible.
+  const int kb0 = sp * a.split_keys;
+  const int key_end = a.nsplit > 1 ? min(a.Skv, kb0 + a.split_keys) : a.Skv;
+  const int kw = kb0 + wave * KW;
+  const int rows_here = min(key_end - kw, KW);  // <= 0: no key for this wavefront
+  _Float16* slice = lds + wave * (L::kSliceB / 2);
+  constexpr uint32_t kOob = 0x80000000u;
+  if (rows_here > 0) {
+    const Rsrc rk = make_rsrc(a.k + b * a.k_sb + kvh * a.k_sh + static_cast<int64_t>(kw) * a.k_ss, kBufRange);
+    const Rsrc rv = make_rsrc(a.v + b * a.v_sb + kvh * a.v_sh + static_cast<int64_t>(kw) * a.v_ss, kBufRange);
+#pragma unroll
+    for (int j = 0; j < L::kNK; ++j) {
+      const int u = 64 * j + lane, row = u / L::kUK, ch = u % L::kUK;
+      const bool ok = row < rows_here && ch < D / 8;  // pads, rows past the keys or the slice: zeros
+      load_lds16(rk, slice + 512 * j,
+                 ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.k_ss) + 8 * ch) * 2 : kOob);
+    }
+#pragma unroll
+    for (int j = 0; j < L::kNV; ++j) {
+      const int u = 64 * j + lane, row = u / (D / 8), ch = u % (D / 8);
+      load_lds16(rv, slice + 512 * (L::kNK + j),
+                 row < rows_here ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_ss) + 8 * ch) * 2 : kOob);
+    }
+  }
+  // Q^T operand: lane (row, half) holds features 16ks + 8half .. +8.
+  f16x8 qv[DK];
+  {
+    const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(qi, a.Sq - 1)) * a.q_ss + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < DK; ++ks) {
+      qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
+      if constexpr (PRESCALED) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[ks][e] = static_cast<_Float16>(static_cast<float>(qv[ks][e]) * a.scale_log2);
+      } else if (a.scale_log2 < 0.f) {
+        qv[ks] = -qv[ks];
+      }
+    }
+  }
+  const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
+  // The wavefront's own slice: its loads landing is all it waits for.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  float m = -INFINITY, l = 0.f;  // m: the rows' max over the slice (log2 units)
+  f32x16 o[DM];
+#pragma unroll
+  for (int dm = 0; dm < DM; ++dm) o[dm] = f32x16{};
+  if (rows_here > 0) {
+    // S^T tile mt: keys 32mt .. 32mt + 31 of the slice; lane (row, half)
+    // holds keys key32_of(8i + 4half + v) in register 4i + v.
+    f32x16 s[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const _Float16* krow = slice + (mt * 32 + key32_of(col)) * L::kRowK + 8 * half;
+      s[mt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < DK; ++ks)
+        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const f16x8*>(krow + 16 * ks), qv[ks], s[mt],
+                                                       0, 0, 0);
+    }
+    // Keys past the run (and past Skv) are masked; scores in log2 units.
+    const int kl = key_end - 1 - kw - 8 * half;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int kr = mt * 32 + key32_of(8 * (rr >> 2) + (rr & 3));
+        const float x = PRESCALED ? s[mt][rr] : s[mt][rr] * scale_abs;
+        s[mt][rr] = kr <= kl ? x : -INFINITY;
+      }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, s[mt][rr]);
+    m = max_xor32(mx);  // the row's max over both lane halves (finite: key kw is visible)
+    // P (fp16) and its row sum over the same fp16 values; pb[mt][j] is the
+    // PV operand of keys 32mt + 16j + 8half .. + 7.
+    f16x8 pb[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[mt][j][e] = static_cast<_Float16>(fast_exp2(s[mt][8 * j + e] - m));
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          l = __builtin_amdgcn_fdot2(f16x2{pb[mt][j][2 * e], pb[mt][j][2 * e + 1]}, f16x2{1, 1}, l, false);
+      }
+    // O^T += V^T P^T: V^T operands by transposing reads of the V slice (rows
+    // of D halves).
+    const uint32_t vtr = static_cast<uint32_t>(wave * (L::kSliceB / 2) + L::kNK * 512) +
+                         static_cast<uint32_t>((8 * half + ((lane & 15) >> 2)) * D + 16 * ((lane >> 4) & 1) +
+                                               4 * (lane & 3));
+#pragma unroll
+    for (int c = 0; c < KW / 16; ++c)
+#pragma unroll
+      for (int dm = 0; dm < DM; ++dm) {
+        const uint32_t e = vtr + 16 * c * D + 32 * dm;
+        const v4i16 lo = tr_read4(lds + e), hi = tr_read4(lds + e + 4 * D);
+        const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c >> 1][c & 1], o[dm], 0, 0, 0);
+      }
+  }
+
+  // Fold: every wavefront's partial (O^T relative to m, m, l per lane) to
+  // LDS over the slices, then thread t folds lane t % 64's values k = V (t /
+  // 64) .. + V - 1 over the 8 partials in wavefront order.
+  __syncthreads();  // every wavefront is done with its slice
+  float* rec = reinterpret_cast<float*>(lds);
+  constexpr int kF = L::kFoldF;
+  {
+    float* mine = rec + (wave * 64 + lane) * kF;
+#pragma unroll
+    for (int dm = 0; dm < DM; ++dm)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) mine[dm * 16 + k] = o[dm][k];
+    mine[D / 2] = m;
+    mine[D / 2 + 1] = l;
+  }
+  __syncthreads();
+  constexpr int V = D / 2 / kWaves2;  // values per thread
+  const int fl = threadIdx.x % 64, part = threadIdx.x / 64;
+  const int fcol = fl & 31, fhalf = fl >> 5;
+  const int fqi = fcol / pack, fh = kvh * a.g + gi * pack + (fcol - fqi * pack);
+  if (fqi >= a.Sq) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves2; ++w) M = fmaxf(M, rec[(w * 64 + fl) * kF + D / 2]);
+  float wt[kWaves2], lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves2; ++w) {
+    const float mw = rec[(w * 64 + fl) * kF + D / 2];
+    wt[w] = mw == -INFINITY ? 0.f : fast_exp2(mw - M);  // a slice without keys weighs 0
+    // the row sum over both lane halves
+    lsum += (rec[(w * 64 + fl) * kF + D / 2 + 1] + rec[(w * 64 + (fl ^ 32)) * kF + D / 2 + 1]) * wt[w];
+  }
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    acc[v] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves2; ++w) acc[v] += rec[(w * 64 + fl) * kF + part * V + v] * wt[w];
+  }
+  // Value k of lane (row, half) is O^T row d = 32 (k / 16) + 8 (k % 16 / 4) + 4 half + k % 4.
+  auto d_of = [&](int k) { return 32 * (k >> 4) + 8 * ((k & 15) >> 2) + 4 * fhalf + (k & 3); };
+  if (a.nsplit > 1) {
+    const int64_t prow = ((static_cast<int64_t>(b) * a.Hq + fh) * a.Sq + fqi) * a.nsplit + sp;
+    float* po = a.part + prow * D;
+#pragma unroll
+    for (int v = 0; v < V; ++v) po[d_of(part * V + v)] = acc[v];
+    if (part == 0 && fhalf == 0) {
+      float* pml = a.part + static_cast<int64_t>(a.B) * a.Hq * a.Sq * a.nsplit * D + 2 * prow;
+      pml[0] = M;
+      pml[1] = lsum;
+    }
+    return;
+  }
+  _Float16* op = a.out + ((static_cast<int64_t>(b) * a.Sq + fqi) * a.Hq + fh) * D;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) op[d_of(part * V + v)] = static_cast<_Float16>(acc[v] * inv);
+  if (a.lse && part == 0 && fhalf == 0)
+    a.lse[(static_cast<int64_t>(b) * a.Hq + fh) * a.Sq + fqi] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
+}
+
 // Combines a key split's partials per (sequence, q head, query): one
 // workgroup per row.  Thread (sl, d4) folds splits sl, sl + SL, ... of
 // features 4 d4 .. 4 d4 + 3, G of them loaded at once (every load issued
@@ -1247,12 +1463,30 @@ int64_t blocks_for(int B, int Hkv, int g, int Sq, int pack) {
 struct GridPlan {
   int pack = 1, nsplit = 1, split_keys = 0;
   size_t part_bytes = 0;
+  bool short_decode = false;  // sdpa_decode_short_kernel
 };
 
 GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, size_t ws_bytes) {
   GridPlan gp;
   const int g = Hq / Hkv;
   gp.split_keys = Skv;
+  // Short decode: one row tile (the g q heads of a KV head times Sq <= 32
+  // rows) whose keys fit one block (kWaves2 slices), or a split of them
+  // over blocks that all run in one round of the device.
+  if (!causal && Sq > 0 && static_cast<int64_t>(g) * Sq <= 32) {
+    const int per_block = kWaves2 * (D == 64 ? ShortLds<64>::kKW : ShortLds<128>::kKW);
+    const int ns = std::max(1, (Skv + per_block - 1) / per_block);
+    const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+    const size_t pb = split_bytes(static_cast<int64_t>(B) * Hq * Sq, ns, D);
+    if (static_cast<int64_t>(B) * Hkv * ns <= cus && (ns == 1 || ws_bytes >= pb)) {
+      gp.pack = g;
+      gp.nsplit = ns;
+      gp.split_keys = ns > 1 ? per_block : Skv;
+      gp.part_bytes = pb;
+      gp.short_decode = true;
+      return gp;
+    }
+  }
   if (!causal && Sq > 0) {
     const int p0 = Sq < kQB ? g : 1;
     int keys = Skv;
@@ -1268,6 +1502,18 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
   }
   gp.pack = pack_heads(B, Hkv, g, Sq);
   return gp;
+}
+
+void launch_short(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
+  const dim3 grid(f2.n_items);
+  if (D == 128 && prescaled)
+    sdpa_decode_short_kernel<128, true><<<grid, kThreads2, 0, st>>>(f2);
+  else if (D == 128)
+    sdpa_decode_short_kernel<128, false><<<grid, kThreads2, 0, st>>>(f2);
+  else if (prescaled)
+    sdpa_decode_short_kernel<64, true><<<grid, kThreads2, 0, st>>>(f2);
+  else
+    sdpa_decode_short_kernel<64, false><<<grid, kThreads2, 0, st>>>(f2);
 }
 
 template <int MK, int SLOTS = 2, bool HALF = false>
@@ -1603,7 +1849,9 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.m_sh = m_sh;
     f2.m_sq = m_sq;
     f2.m_bytes = static_cast<uint32_t>(mp.span);
-    if (mask_kind == kMaskF16)
+    if (gpl.short_decode)
+      launch_short(f2, D, prescaled, st);  // one row tile, its keys all in flight at once
+    else if (mask_kind == kMaskF16)
       launch_lds<kMaskF16>(f2, D, prescaled, st);
     else if (mask_kind == kMaskBool)
       launch_lds<kMaskBool>(f2, D, prescaled, st);
