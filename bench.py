@@ -162,7 +162,7 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     gg = torch.Generator(device=dev).manual_seed(seed + 1)
 
     # dense MHA decode: q [1, 8, 1, 64], k/v [1, 8, 512, 64], scale 1/8 (launch-bound:
-    # absolute µs; 8 key splits of one 64-key step, then the merge kernel)
+    # absolute µs; one short-decode kernel, a block per head)
     q1 = torch.randn((1, 8, 1, 64), generator=gg, device=dev).half()
     k1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
     v1 = torch.randn((1, 8, 512, 64), generator=gg, device=dev).half()
@@ -171,7 +171,7 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
     ms_p = timed(lambda i: call1(), steps, warmup, stream)
     res["dense_mha_decode_b1_h8_s512_d64"] = {"us_per_call": round(ms * 1e3, 2),
                                                "us_per_call_prepared": round(ms_p * 1e3, 2),
-                                               "algorithmic_bytes": 1_050_624}
+                                               "algorithmic_bytes": 1_050_624, "kernels_per_step": 1}
     # the Llama-3-8B decode step through SDPA with dense (unpaged) K/V:
     # q [32, 32, 1, 128], k/v [32, 8, 4096, 128] (the q heads of a KV head
     # packed into one block's rows)
