@@ -584,3 +584,32 @@ def test_stream_pointer_follows_current_stream(cuda):
         assert _stream_ptr(cuda) == s.cuda_stream
         assert _stream_ptr(torch.device("cuda")) == s.cuda_stream
     assert _stream_ptr(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+
+
+def _short_decode_shapes(n, seed):
+    """Seeded shapes in the short-decode domain (g q heads x Sq <= 32 rows
+    per block): batch, KV heads, group, Sq, D, key count (0 .. 3000, most
+    not a multiple of a slice) and a row padding for q and k."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        g = int(rng.choice([1, 2, 4, 8]))
+        sq = int(rng.integers(1, 32 // g + 1))
+        out.append((int(rng.integers(1, 4)), int(rng.choice([1, 2, 4, 8])), g, sq, int(rng.choice([64, 128])),
+                    int(rng.integers(0, 3001)), int(rng.choice([0, 8, 32]))))
+    return out
+
+
+@pytest.mark.parametrize("B,Hkv,g,Sq,D,Skv,pad", _short_decode_shapes(16, SEED + 90), ids=str)
+def test_short_decode_random_shapes(cuda, B, Hkv, g, Sq, D, Skv, pad):
+    Hq = Hkv * g
+    q = randn((B, Hq, Sq, D + pad), SEED + 91 + Skv)[..., :D]
+    k = randn((B, Hkv, Skv, D + pad), SEED + 92)[..., :D]
+    v = randn((B, Hkv, Skv, D), SEED + 93)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    if Skv == 0:
+        assert not out.float().abs().sum() and bool(torch.isneginf(lse.cpu()).all())
+        return
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
