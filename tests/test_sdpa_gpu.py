@@ -613,3 +613,23 @@ def test_short_decode_random_shapes(cuda, B, Hkv, g, Sq, D, Skv, pad):
     assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
     _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
     assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("Sq,Skv,causal", [(300, 200, False), (300, 300, True), (1, 700, False), (4, 130, False)])
+def test_keys_expanded_along_the_sequence(cuda, Sq, Skv, causal):
+    """K and V expanded from one row ([B, Hkv, 1, D] with sequence stride 0):
+    every key is the same, so each row's output is that value row and its
+    LSE is scale q.k + ln(visible keys); prefill (full, causal) and the
+    short-decode kernel."""
+    B, Hq, Hkv, D = 2, 8, 2, 128
+    q = randn((B, Hq, Sq, D), SEED + 95)
+    k1, v1 = randn((B, Hkv, 1, D), SEED + 96), randn((B, Hkv, 1, D), SEED + 97)
+    k, v = k1.to(cuda).expand(B, Hkv, Skv, D), v1.to(cuda).expand(B, Hkv, Skv, D)
+    assert k.stride(2) == 0
+    out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
+    g = Hq // Hkv
+    want = v1.float().repeat_interleave(g, dim=1).expand(B, Hq, Sq, D)
+    assert_close(out, want)
+    s = (q.double() @ k1.double().repeat_interleave(g, dim=1).transpose(-1, -2))[..., 0] / math.sqrt(D)
+    visible = torch.arange(Sq, dtype=torch.float64).add(1).clamp(max=Skv) if causal else torch.full((Sq,), float(Skv))
+    assert np.allclose(lse.cpu().double().numpy(), (s + visible.log()).numpy(), atol=LSE_ATOL, rtol=0)

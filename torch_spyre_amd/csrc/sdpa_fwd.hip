@@ -517,39 +517,45 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   static_assert(kKT * kUK % 64 == 0 && kKT * kUV % 64 == 0, "tiles must be whole loads");
   constexpr int kJK = (kNK + kWaves2 - 1) / kWaves2, kJV = (kNV + kWaves2 - 1) / kWaves2;
   constexpr uint32_t kOob = 0x80000000u;  // past kBufRange
-  uint32_t k_off[kJK], k_row[kJK], v_off[kJV], v_row[kJV];
+  uint32_t k_off[kJK], v_off[kJV];
 #pragma unroll
   for (int j = 0; j < kJK; ++j) {
     const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUK, ch = u % kUK;
     const bool pad = ch == kUK - 1;
-    k_row[j] = pad ? kOob : static_cast<uint32_t>(row);
     k_off[j] = pad ? kOob : (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.k_ss) + 8 * ch) * 2;
   }
 #pragma unroll
   for (int j = 0; j < kJV; ++j) {
     const int u = 64 * (wave + kWaves2 * j) + lane, row = u / kUV, ch = u % kUV;
     const bool pad = ch >= D / 8;  // kRowV / 8 - D / 8 pad units per row
-    v_row[j] = pad ? kOob : static_cast<uint32_t>(row);
     v_off[j] = pad ? kOob : (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_ss) + 8 * ch) * 2;
   }
-  // K rows kb .. kb + 63 into slot `slot` (rows >= Skv as zeros).
+  // K rows kb .. kb + 63 into slot `slot`.  The descriptor's range ends
+  // with row Skv - 1, so rows past it arrive as zeros without a per-lane
+  // test (no unit straddles the end: a row's units end within its stride).
+  // With a key stride of 0 every row reads row 0's bytes, finite values
+  // the key test masks.
   auto dma_k = [&](int kb, int slot) {
-    const Rsrc r = make_rsrc(kbase + static_cast<int64_t>(kb) * a.k_ss, kBufRange);
-    const uint32_t rows_left = static_cast<uint32_t>(a.Skv - kb);
+    const uint32_t range =
+        a.k_ss > 0 ? static_cast<uint32_t>(min(static_cast<int64_t>(kBufRange), static_cast<int64_t>(a.Skv - kb) * a.k_ss * 2))
+                   : kBufRange;  // a key stride of 0 (expanded): every row is row 0
+    const Rsrc r = make_rsrc(kbase + static_cast<int64_t>(kb) * a.k_ss, range);
 #pragma unroll
     for (int j = 0; j < kJK; ++j)
       if (wave + kWaves2 * j < kNK)
-        load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_row[j] < rows_left ? k_off[j] : kOob);
+        load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_off[j]);
   };
-  // V rows kb .. kb + 63 into slot `slot` (rows >= Skv as zeros, so that a
-  // masked key's P = 0 never meets stale bits).
+  // V rows kb .. kb + 63 into slot `slot` (rows past Skv as zeros, the same
+  // way, so that a masked key's P = 0 never meets stale bits).
   auto dma_v = [&](int kb, int slot) {
-    const Rsrc r = make_rsrc(vbase + static_cast<int64_t>(kb) * a.v_ss, kBufRange);
-    const uint32_t rows_left = static_cast<uint32_t>(a.Skv - kb);
+    const uint32_t range =
+        a.v_ss > 0 ? static_cast<uint32_t>(min(static_cast<int64_t>(kBufRange), static_cast<int64_t>(a.Skv - kb) * a.v_ss * 2))
+                   : kBufRange;  // a key stride of 0 (expanded): every row is row 0
+    const Rsrc r = make_rsrc(vbase + static_cast<int64_t>(kb) * a.v_ss, range);
 #pragma unroll
     for (int j = 0; j < kJV; ++j)
       if (wave + kWaves2 * j < kNV)
-        load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_row[j] < rows_left ? v_off[j] : kOob);
+        load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_off[j]);
   };
   // The wavefront's mask block of keys kb .. kb + 63 into its slot `slot`:
   // rows past Sq and bytes past the (sequence, head) slice arrive as zeros.
