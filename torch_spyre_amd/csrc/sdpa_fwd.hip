@@ -530,32 +530,39 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     const bool pad = ch >= D / 8;  // kRowV / 8 - D / 8 pad units per row
     v_off[j] = pad ? kOob : (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_ss) + 8 * ch) * 2;
   }
-  // K rows kb .. kb + 63 into slot `slot`.  The descriptor's range ends
-  // with row Skv - 1, so rows past it arrive as zeros without a per-lane
-  // test (no unit straddles the end: a row's units end within its stride).
-  // With a key stride of 0 every row reads row 0's bytes, finite values
-  // the key test masks.
-  auto dma_k = [&](int kb, int slot) {
-    const uint32_t range =
-        a.k_ss > 0 ? static_cast<uint32_t>(min(static_cast<int64_t>(kBufRange), static_cast<int64_t>(a.Skv - kb) * a.k_ss * 2))
-                   : kBufRange;  // a key stride of 0 (expanded): every row is row 0
-    const Rsrc r = make_rsrc(kbase + static_cast<int64_t>(kb) * a.k_ss, range);
+  // K / V tiles load in sequence (K(0), K(1), ... and V(0), V(1), ...), so
+  // each has a running cursor: the next tile's first row and the bytes from
+  // it to the end of row Skv - 1.  Rows past Skv lie past the descriptor's
+  // range and arrive as zeros without a per-lane test (no unit straddles
+  // the end: a row's units end within its stride); with a key stride of 0
+  // every row reads row 0's bytes, finite values the key test masks.
+  const _Float16* k_cur = kbase + static_cast<int64_t>(sp) * a.split_keys * a.k_ss;
+  const _Float16* v_cur = vbase + static_cast<int64_t>(sp) * a.split_keys * a.v_ss;
+  int64_t k_left = (static_cast<int64_t>(a.Skv) - static_cast<int64_t>(sp) * a.split_keys) * a.k_ss * 2;
+  int64_t v_left = (static_cast<int64_t>(a.Skv) - static_cast<int64_t>(sp) * a.split_keys) * a.v_ss * 2;
+  const int64_t k_tile = static_cast<int64_t>(kKT) * a.k_ss, v_tile = static_cast<int64_t>(kKT) * a.v_ss;
+  auto range_of = [](int64_t left, int64_t ss) {
+    return ss > 0 ? static_cast<uint32_t>(min(max(left, int64_t{0}), static_cast<int64_t>(kBufRange))) : kBufRange;
+  };
+  // The next K tile into slot `slot`.
+  auto dma_k = [&](int slot) {
+    const Rsrc r = make_rsrc(k_cur, range_of(k_left, a.k_ss));
 #pragma unroll
     for (int j = 0; j < kJK; ++j)
-      if (wave + kWaves2 * j < kNK)
-        load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_off[j]);
+      if (wave + kWaves2 * j < kNK) load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_off[j]);
+    k_cur += k_tile;
+    k_left -= 2 * k_tile;
   };
-  // V rows kb .. kb + 63 into slot `slot` (rows past Skv as zeros, the same
-  // way, so that a masked key's P = 0 never meets stale bits).
-  auto dma_v = [&](int kb, int slot) {
-    const uint32_t range =
-        a.v_ss > 0 ? static_cast<uint32_t>(min(static_cast<int64_t>(kBufRange), static_cast<int64_t>(a.Skv - kb) * a.v_ss * 2))
-                   : kBufRange;  // a key stride of 0 (expanded): every row is row 0
-    const Rsrc r = make_rsrc(vbase + static_cast<int64_t>(kb) * a.v_ss, range);
+  // The next V tile into slot `slot` (rows past Skv as zeros, so that a
+  // masked key's P = 0 never meets stale bits).
+  auto dma_v = [&](int slot) {
+    const Rsrc r = make_rsrc(v_cur, range_of(v_left, a.v_ss));
 #pragma unroll
     for (int j = 0; j < kJV; ++j)
       if (wave + kWaves2 * j < kNV)
         load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_off[j]);
+    v_cur += v_tile;
+    v_left -= 2 * v_tile;
   };
   // The wavefront's mask block of keys kb .. kb + 63 into its slot `slot`:
   // rows past Sq and bytes past the (sequence, head) slice arrive as zeros.
@@ -842,13 +849,13 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   auto step_h = [&](int t, f32x16& cur, f32x16& nxt) {
     const _Float16* k1 = lds + ((t + 1) % SLOTS) * L::kSlot;
     if constexpr (SLOTS == 2) {
-      if (t + 2 < n_tiles) dma_k(kb0 + (t + 2) * kKT, t & 1);
-      if (t + 1 < n_tiles) dma_v(kb0 + (t + 1) * kKT, (t + 1) & 1);
+      if (t + 2 < n_tiles) dma_k(t & 1);
+      if (t + 1 < n_tiles) dma_v((t + 1) & 1);
     } else if ((t & 1) == 0) {
-      if (t + 3 < n_tiles) dma_k(kb0 + (t + 3) * kKT, (t + 3) % 4);
-      if (t + 4 < n_tiles) dma_k(kb0 + (t + 4) * kKT, t % 4);
-      if (t + 2 < n_tiles) dma_v(kb0 + (t + 2) * kKT, (t + 2) % 4);
-      if (t + 3 < n_tiles) dma_v(kb0 + (t + 3) * kKT, (t + 3) % 4);
+      if (t + 3 < n_tiles) dma_k((t + 3) % 4);
+      if (t + 4 < n_tiles) dma_k(t % 4);
+      if (t + 2 < n_tiles) dma_v((t + 2) % 4);
+      if (t + 3 < n_tiles) dma_v((t + 3) % 4);
     }
     if (active(t)) {
       vtr = static_cast<uint32_t>((t % SLOTS) * L::kSlot + L::kK) + vtr_lane;
@@ -921,18 +928,18 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
     if constexpr (SLOTS == 2) {
       // K(t+2) replaces K(t) (read during step t-1), V(t+1) replaces
       // V(t-1); both land during this step's math.
-      if (t + 2 < n_tiles) dma_k(kb0 + (t + 2) * kKT, t & 1);
-      if (t + 1 < n_tiles) dma_v(kb0 + (t + 1) * kKT, (t + 1) & 1);
+      if (t + 2 < n_tiles) dma_k(t & 1);
+      if (t + 1 < n_tiles) dma_v((t + 1) & 1);
       if (t + 1 < n_tiles) dma_m(kb0 + (t + 1) * kKT, (t + 1) & 1);
     } else if ((t & 1) == 0) {
       // Steps t, t + 1 read K(t+1), K(t+2), V(t), V(t+1) (slot = tile % 4);
       // K(t+3), K(t+4), V(t+2), V(t+3) fill the other four slot halves,
       // whose last readers were steps t - 2 and t - 1, and land by the
       // barrier after step t + 1.
-      if (t + 3 < n_tiles) dma_k(kb0 + (t + 3) * kKT, (t + 3) % 4);
-      if (t + 4 < n_tiles) dma_k(kb0 + (t + 4) * kKT, t % 4);
-      if (t + 2 < n_tiles) dma_v(kb0 + (t + 2) * kKT, (t + 2) % 4);
-      if (t + 3 < n_tiles) dma_v(kb0 + (t + 3) * kKT, (t + 3) % 4);
+      if (t + 3 < n_tiles) dma_k((t + 3) % 4);
+      if (t + 4 < n_tiles) dma_k(t % 4);
+      if (t + 2 < n_tiles) dma_v((t + 2) % 4);
+      if (t + 3 < n_tiles) dma_v((t + 3) % 4);
     }
     if (active(t)) {
       vtr = static_cast<uint32_t>((t % SLOTS) * L::kSlot + L::kK) + vtr_lane;
@@ -1033,14 +1040,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // before it is, so S is never read unwritten.
   f32x16 sa[2], sb[2];
   if (n_tiles > 0) {
-    dma_k(kb0, 0);
-    dma_v(kb0, 0);
+    dma_k(0);
+    dma_v(0);
     dma_m(kb0, 0);
   }
-  if (n_tiles > 1) dma_k(kb0 + kKT, 1);
+  if (n_tiles > 1) dma_k(1);
   if constexpr (SLOTS == 4) {
-    if (n_tiles > 1) dma_v(kb0 + kKT, 1);
-    if (n_tiles > 2) dma_k(kb0 + 2 * kKT, 2);
+    if (n_tiles > 1) dma_v(1);
+    if (n_tiles > 2) dma_k(2);
   }
   dma_wait();
   __syncthreads();
