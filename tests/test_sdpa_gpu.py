@@ -633,3 +633,29 @@ def test_keys_expanded_along_the_sequence(cuda, Sq, Skv, causal):
     s = (q.double() @ k1.double().repeat_interleave(g, dim=1).transpose(-1, -2))[..., 0] / math.sqrt(D)
     visible = torch.arange(Sq, dtype=torch.float64).add(1).clamp(max=Skv) if causal else torch.full((Sq,), float(Skv))
     assert np.allclose(lse.cpu().double().numpy(), (s + visible.log()).numpy(), atol=LSE_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("Sq", [1, 70])
+def test_key_stride_near_the_descriptor_limit(cuda, Sq):
+    """K and V rows 2^29 elements (1 GiB) apart, 2 keys: the head's span
+    ends just inside one 2 GiB buffer descriptor while Skv x stride passes
+    it, so the tile loads' byte counts start clamped; prefill and the
+    short-decode kernel."""
+    D, ss = 128, 1 << 29
+    q = randn((1, 2, Sq, D), SEED + 98)
+    kv = []
+    for s in (SEED + 99, SEED + 100):
+        base = torch.zeros(ss + D, dtype=torch.float16, device=cuda)
+        rows = randn((2, D), s)
+        base[:D] = rows[0].to(cuda)
+        base[ss:] = rows[1].to(cuda)
+        kv.append(base.as_strided((1, 1, 2, D), (0, 0, ss, 1)))
+    k, v = kv
+    assert k.stride(2) * 2 * 2 > 0x7FFFFFF0 >= ((k.shape[2] - 1) * k.stride(2) + D) * 2
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    kc, vc = k.cpu(), v.cpu()
+    assert_close(out, OA.sdpa_cpu_fp32(q, kc, vc))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, kc, vc, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+    del k, v, kv
+    torch.cuda.empty_cache()

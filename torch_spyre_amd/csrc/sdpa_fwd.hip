@@ -538,31 +538,38 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
   // every row reads row 0's bytes, finite values the key test masks.
   const _Float16* k_cur = kbase + static_cast<int64_t>(sp) * a.split_keys * a.k_ss;
   const _Float16* v_cur = vbase + static_cast<int64_t>(sp) * a.split_keys * a.v_ss;
-  int64_t k_left = (static_cast<int64_t>(a.Skv) - static_cast<int64_t>(sp) * a.split_keys) * a.k_ss * 2;
-  int64_t v_left = (static_cast<int64_t>(a.Skv) - static_cast<int64_t>(sp) * a.split_keys) * a.v_ss * 2;
   const int64_t k_tile = static_cast<int64_t>(kKT) * a.k_ss, v_tile = static_cast<int64_t>(kKT) * a.v_ss;
-  auto range_of = [](int64_t left, int64_t ss) {
-    return ss > 0 ? static_cast<uint32_t>(min(max(left, int64_t{0}), static_cast<int64_t>(kBufRange))) : kBufRange;
+  // Bytes left as 32-bit values: the head's whole span fits one descriptor
+  // (< 2 GiB, checked by the host), so a count clamped to kBufRange at the
+  // start still covers every valid row and no row past Skv.
+  auto left0 = [&](int64_t ss) {
+    if (ss == 0) return static_cast<int32_t>(kBufRange);
+    const int64_t all = static_cast<int64_t>(a.Skv) * ss * 2;
+    return static_cast<int32_t>(min(all, static_cast<int64_t>(kBufRange)) - static_cast<int64_t>(sp) * a.split_keys * ss * 2);
   };
+  int32_t k_left = left0(a.k_ss), v_left = left0(a.v_ss);
+  const int32_t k_step = static_cast<int32_t>(min(2 * k_tile, static_cast<int64_t>(kBufRange)));
+  const int32_t v_step = static_cast<int32_t>(min(2 * v_tile, static_cast<int64_t>(kBufRange)));
+  auto range_of = [](int32_t left) { return static_cast<uint32_t>(max(left, 0)); };
   // The next K tile into slot `slot`.
   auto dma_k = [&](int slot) {
-    const Rsrc r = make_rsrc(k_cur, range_of(k_left, a.k_ss));
+    const Rsrc r = make_rsrc(k_cur, range_of(k_left));
 #pragma unroll
     for (int j = 0; j < kJK; ++j)
       if (wave + kWaves2 * j < kNK) load_lds16(r, lds + slot * L::kSlot + 512 * (wave + kWaves2 * j), k_off[j]);
     k_cur += k_tile;
-    k_left -= 2 * k_tile;
+    k_left -= k_step;
   };
   // The next V tile into slot `slot` (rows past Skv as zeros, so that a
   // masked key's P = 0 never meets stale bits).
   auto dma_v = [&](int slot) {
-    const Rsrc r = make_rsrc(v_cur, range_of(v_left, a.v_ss));
+    const Rsrc r = make_rsrc(v_cur, range_of(v_left));
 #pragma unroll
     for (int j = 0; j < kJV; ++j)
       if (wave + kWaves2 * j < kNV)
         load_lds16(r, lds + slot * L::kSlot + L::kK + 512 * (wave + kWaves2 * j), v_off[j]);
     v_cur += v_tile;
-    v_left -= 2 * v_tile;
+    v_left -= v_step;
   };
   // The wavefront's mask block of keys kb .. kb + 63 into its slot `slot`:
   // rows past Sq and bytes past the (sequence, head) slice arrive as zeros.
