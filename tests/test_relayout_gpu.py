@@ -395,3 +395,25 @@ def test_stepped_transpose_from_strided_host_vs_oracle(cuda):
     back = tsa.from_device_layout(dev)
     torch.cuda.synchronize()
     assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))
+
+
+# Narrow stick tiles: a loop of 8, 16 or 24 sticks beside the stick (host
+# dim 0 of a default layout: a batch of 8, a KV cache of 8 sequences) moves
+# in 8 x 128 / 16 x 64 tiles one way and 128 x 8 / 64 x 16 the other.
+NARROW_CASES = [([8, 1024, 4096], None), ([16, 256, 2048], None), ([24, 128, 1024], None),
+                ([8, 8, 2048, 128], None), ([8, 3, 64, 4096], {2: 72})]
+
+
+@pytest.mark.parametrize("sizes,pad", NARROW_CASES, ids=str)
+def test_narrow_stick_tiles_vs_oracle(cuda, sizes, pad):
+    import torch_spyre_amd as tsa
+
+    x, store, strides, off = _host_view(sizes, pad, SEED + 450 + sum(sizes), cuda)
+    order = list(range(len(sizes)))
+    stl = tsa.SpyreTensorLayout(list(sizes), strides, torch.float16, order)
+    dev = tsa.to_device_layout(x, stl)
+    want = OL.h2d(store, list(sizes), strides, off, OL.stl_init(list(sizes), strides, "float16", order))
+    assert np.array_equal(_as_bits(dev).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    torch.cuda.synchronize()
+    assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))

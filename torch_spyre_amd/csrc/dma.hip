@@ -887,7 +887,14 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
         if (outer[k].sd == row && ai < 0) ai = static_cast<int>(k);
         else if (outer[k].ss == row && bi < 0) bi = static_cast<int>(k);
       }
-      if (ai >= 0 && bi >= 0 && outer[ai].size >= kTileSticks && outer[bi].size >= kTileSticks) {
+      // A narrow A or B loop (8, 16 or 24 sticks: a batch dim of 8 above the
+      // stick, a KV cache of 8 sequences) takes 8 x 128 or 16 x 64 stick
+      // tiles (128 x 8 or 64 x 16 for B), whole tiles only.
+      auto narrow = [](int64_t size) { return size < kTileSticks && size % 8 == 0; };
+      const bool wide_a = ai >= 0 && outer[ai].size >= kTileSticks, wide_b = bi >= 0 && outer[bi].size >= kTileSticks;
+      const bool narrow_a = wide_b && ai >= 0 && narrow(outer[ai].size);
+      const bool narrow_b = wide_a && bi >= 0 && narrow(outer[bi].size);
+      if ((wide_a && wide_b) || narrow_a || narrow_b) {
         SNest n{};
         n.na = static_cast<uint32_t>(outer[ai].size);
         n.nb = static_cast<uint32_t>(outer[bi].size);
@@ -898,7 +905,11 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
         // [4096, 4096]; the 32 x 32 tile with interleaved stores is best for
         // row-major -> sticks).
         const bool tall = n.na == 64 && outer[bi].sd == 64 * row;
-        const uint32_t TA = tall ? 64 : kTileSticks, TB = tall ? 16 : kTileSticks;
+        const uint32_t TA = narrow_a   ? (n.na == 16 ? 16 : 8)
+                            : narrow_b ? (n.nb == 16 ? 64 : 128)
+                            : tall     ? 64
+                                       : kTileSticks;
+        const uint32_t TB = 1024 / TA;
         const uint32_t ta = (n.na + TA - 1) / TA;
         const uint32_t tb = (n.nb + TB - 1) / TB;
         int64_t tiles = int64_t{ta} * tb;
@@ -932,9 +943,21 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
           auto step_go = [&](auto nl_c) {
             constexpr int NL = decltype(nl_c)::value;
             const StepNest<NL> x = make_step<NL>(tl, tiles, off_s, off_d, sp.span_s, sp.span_d, n.a_ss, n.b_sd);
-            if (tall && sp.pow2)
+            if (narrow_a && TA == 8 && sp.pow2)
+              dma_stick_step_kernel<8, 128, true, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (narrow_a && TA == 8)
+              dma_stick_step_kernel<8, 128, true, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (narrow_a && sp.pow2)
+              dma_stick_step_kernel<16, 64, true, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (narrow_a)
+              dma_stick_step_kernel<16, 64, true, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (TA == 128 && sp.pow2)
+              dma_stick_step_kernel<128, 8, true, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (TA == 128)
+              dma_stick_step_kernel<128, 8, true, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
+            else if (TA == 64 && sp.pow2)
               dma_stick_step_kernel<64, 16, true, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
-            else if (tall)
+            else if (TA == 64)
               dma_stick_step_kernel<64, 16, true, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x);
             else if (sp.pow2)
               dma_stick_step_kernel<32, 32, false, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x);
@@ -949,7 +972,7 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
           }
           return check_launch("dma_stick_step_kernel");
         }
-        if (tiles < (int64_t{1} << 31)) {
+        if (!narrow_a && !narrow_b && tiles < (int64_t{1} << 31)) {  // narrow nests with edges: the vec kernel
           const dim3 grid(static_cast<uint32_t>(tiles));
           // 32-bit buffer offsets when a tile's spans fit them
           const bool buf = (int64_t{TA} - 1) * n.a_ss + int64_t{TB} * row < int64_t{kBufRange} &&
