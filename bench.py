@@ -23,7 +23,8 @@ prefill SDPA, causal, full and with an fp16 / boolean [4096, 4096] mask
 [8192, 8192] GEMM (the MFMA rate a plain library GEMM reaches on the box);
 under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
 transpose-restick, rotating 9 buffer pairs (576 MiB), with torch's CPU
-view/permute/contiguous of the same closed forms as its CPU baseline.
+view/permute/contiguous of the same closed forms as its CPU baseline, and
+a KV cache of 8 sequences [8, 8, 2048, 128] to and from its default layout.
 
 Timing: HIP events on the stream the kernels are launched on, around K
 back-to-back steps, after W warm-up steps.  GB/s = algorithmic bytes / time.
@@ -398,6 +399,27 @@ def main():
     flat = [DmaCopy(xs[i], outs_host[i], tsa.relayout.flat_plan(R * C)) for i in range(nbuf)]
     t = timed(lambda i: flat[i % nbuf](), args.steps, args.warmup, stream)
     relayout["flat_copy_reference"] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1)}
+    del devs, outs_dev, outs_host, flat
+    # a KV cache of 8 sequences, [8, 8, 2048, 128] fp16 (32 MiB), to and from its default layout
+    # [8, 2048, 2, 8, 64]: the 8 sequences sit beside the stick (8 x 128 / 128 x 8 stick tiles)
+    kv_size = [8, 8, 2048, 128]
+    kv_st = [8 * 2048 * 128, 2048 * 128, 128, 1]
+    kv_lay = tsa.SpyreTensorLayout(kv_size, torch.float16)
+    kxs = [xb.view(kv_size) for xb in (bits16(i) for i in range(nbuf))]
+    kdevs = [torch.empty(tsa.relayout.alloc_shape(kv_size, torch.float16, kv_lay), dtype=torch.float16, device=dev)
+             for _ in range(nbuf)]
+    kv = {}
+    for name, calls in (
+        ("to_sticks", [DmaCopy(kxs[i], kdevs[i], tsa.dma_plan(kv_size, kv_st, kv_st, 0, kv_lay, True))
+                       for i in range(nbuf)]),
+        ("from_sticks", [DmaCopy(kdevs[i], kxs[i], tsa.dma_plan(kv_size, kv_st, kv_st, 0, kv_lay, False))
+                         for i in range(nbuf)]),
+    ):
+        t = timed(lambda i: calls[i % nbuf](), args.steps, args.warmup, stream)
+        kv[name] = {"us": round(t * 1e3, 3), "GB/s": round(rel_bytes / (t * 1e-3) / 1e9, 1),
+                    "frac": round(rel_bytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    relayout["kv_cache_b8_h8_s2048_d128"] = kv
+    del kxs, kdevs
 
     result = {
         "metric": METRIC,
