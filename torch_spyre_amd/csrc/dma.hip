@@ -1055,9 +1055,33 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
         if (ta > 1) tl.push_back({ta, 128, 64 * A.sd});
         if (tb > 1) tl.push_back({tb, 64 * B.ss, 128});
         for (const Loop& o : outer) tl.push_back(o);
+        // A wavefront's four tiles run along tl[0].  When they are B tiles
+        // (contiguous in dst) and another loop steps by one 128-byte row in
+        // src (a 3-D transpose back to host order: the host dim beside the
+        // stick), that loop goes right after the four, so the four
+        // wavefronts of a workgroup read adjacent src rows: 512-byte runs on
+        // both sides instead of 128-byte src pieces 16 KiB apart (measured
+        // [8, 1024, 4096], dim order [0, 2, 1], back to host order: 35.2 ->
+        // 34.0 us).  With A tiles first the same move cost more than it gave
+        // (27.0 -> 32.3 us the other way): src runs of 2 KiB per workgroup
+        // row matter more there than dst runs of 512 B.
+        if (!tl.empty() && ta <= 1 && tl.size() <= 3 && tl[0].size > kTransposeTiles &&
+            tl[0].size % kTransposeTiles == 0) {
+          for (size_t k = 1; k < tl.size(); ++k) {
+            if (tl[k].ss != 128) continue;
+            const Loop partner = tl[k];
+            tl.erase(tl.begin() + static_cast<std::ptrdiff_t>(k));
+            const Loop first = tl[0];
+            tl[0] = {kTransposeTiles, first.ss, first.sd};
+            tl.insert(tl.begin() + 1, partner);
+            tl.insert(tl.begin() + 2, {first.size / kTransposeTiles, first.ss * kTransposeTiles,
+                                       first.sd * kTransposeTiles});
+            break;
+          }
+        }
         const StepSpan sp = step_span(tl, off_s, off_d, 63 * B.ss + 128, 63 * A.sd + 128);
-        if (sp.ok && n.na % 8 == 0 && n.nb % 8 == 0 && tl[0].size % kTransposeTiles == 0 && A.sd > 0 &&
-            B.ss > 0) {
+        if (sp.ok && !tl.empty() && n.na % 8 == 0 && n.nb % 8 == 0 && tl[0].size % kTransposeTiles == 0 &&
+            A.sd > 0 && B.ss > 0) {
           auto step_go = [&](auto nl_c) {
             constexpr int NL = decltype(nl_c)::value;
             const StepNest<NL> x = make_step<NL>(tl, n.tiles, off_s, off_d, sp.span_s, sp.span_d, B.ss, A.sd);
