@@ -417,3 +417,24 @@ def test_narrow_stick_tiles_vs_oracle(cuda, sizes, pad):
     back = tsa.from_device_layout(dev)
     torch.cuda.synchronize()
     assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("sizes", [[64, 64], [1, 64, 64], [2, 64, 64]], ids=str)
+def test_single_tile_restickify_vs_oracle(cuda, sizes):
+    """A transpose that is one 64 x 64 tile (or one per outer index): no
+    tile loop longer than one."""
+    import torch_spyre_amd as tsa
+
+    order = list(range(len(sizes)))
+    order[-2], order[-1] = order[-1], order[-2]
+    strides = OL.contiguous_strides(sizes)
+    src = tsa.SpyreTensorLayout(sizes, torch.float16)
+    dst = tsa.SpyreTensorLayout(sizes, strides, torch.float16, order)
+    bits = OR.random_finite_f16_bits((int(np.prod(sizes)),), SEED + 470 + sum(sizes))
+    x = _bits_tensor(bits, cuda).view(sizes)
+    out = tsa.restickify(tsa.to_device_layout(x, src), dst)
+    want = OL.h2d(bits, sizes, strides, 0, OL.stl_init(sizes, strides, "float16", order))
+    assert np.array_equal(_as_bits(out).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(tsa.to_device_layout(x, dst))
+    torch.cuda.synchronize()
+    assert torch.equal(back.contiguous().view(torch.int16), x.view(torch.int16))
