@@ -439,6 +439,15 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_kernel(S
 // have been dispatched; ragged batches stay balanced.
 template <int D>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_list_kernel(SplitArgs a) {
+  if (a.max_chunks == 1) {
+    // Every sequence is one chunk (an empty one too): item x is (sequence
+    // x / Hkv, chunk 0, KV head x % Hkv), with no prefix sum to wait for.
+    const int item = blockIdx.x;
+    if (item >= a.B * a.Hkv) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    run_item<D>(a, item / a.Hkv, 0, item % a.Hkv, wave, lane);
+    return;
+  }
   __shared__ int s_pre[kMaxListSeqs > 0 ? kMaxListSeqs + 1 : 1];
   for (int i = threadIdx.x; i < a.B; i += kThreads) {
     const int c = min(max(a.ctx_lens[i], 0), a.max_ctx);
