@@ -438,3 +438,25 @@ def test_single_tile_restickify_vs_oracle(cuda, sizes):
     back = tsa.from_device_layout(tsa.to_device_layout(x, dst))
     torch.cuda.synchronize()
     assert torch.equal(back.contiguous().view(torch.int16), x.view(torch.int16))
+
+
+# A small side (2 .. 31 sticks, no multiple of 8) beside the stick, its
+# other side dense: n rows of T sticks against one dense run per tile, both
+# ways (the dma_stick_small_kernel route).
+SMALL_CASES = [([3, 2048, 4096], None), ([5, 64, 4096], None), ([2, 1024, 2048], None), ([12, 256, 1024], None),
+               ([31, 64, 2048], None), ([4, 8, 2048, 128], None), ([3, 5, 64, 4096], {2: 72})]
+
+
+@pytest.mark.parametrize("sizes,pad", SMALL_CASES, ids=str)
+def test_small_side_stick_tiles_vs_oracle(cuda, sizes, pad):
+    import torch_spyre_amd as tsa
+
+    x, store, strides, off = _host_view(sizes, pad, SEED + 480 + sum(sizes), cuda)
+    order = list(range(len(sizes)))
+    stl = tsa.SpyreTensorLayout(list(sizes), strides, torch.float16, order)
+    dev = tsa.to_device_layout(x, stl)
+    want = OL.h2d(store, list(sizes), strides, off, OL.stl_init(list(sizes), strides, "float16", order))
+    assert np.array_equal(_as_bits(dev).reshape(-1)[: want.size], want)
+    back = tsa.from_device_layout(dev)
+    torch.cuda.synchronize()
+    assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))

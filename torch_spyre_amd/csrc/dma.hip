@@ -42,6 +42,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <type_traits>
 #include <vector>
@@ -424,6 +425,94 @@ __global__ __launch_bounds__(kThreads) void dma_stick_step_kernel(const char* __
     const uint32_t m = WAVE_RUNS ? kPer * wave + k : 4 * k + wave, b = m / (TA / 8), ca = m % (TA / 8);
     store16(rd, v, sd + b * b_sd + ca * 1024, r[k]);
   }
+}
+
+// A stick tile with a small side: n < 32 rows of T contiguous sticks on one
+// side (rows r_stride bytes apart), and the same n x T sticks dense on the
+// other, stick (y, x) at (y n + x) x 128 bytes.  Row-major -> sticks when a
+// host dim of n sits beside the stick (a batch of 3: the n rows are src,
+// the dense block dst), and the way back (D2R).  Per tile, the row side
+// moves n runs of T x 128 bytes and the dense side one run of n T x 128.
+struct SmallTile {
+  uint32_t n, T;      // rows; sticks per row in a tile (a power of two >= 8, n T <= 1024)
+  uint32_t r_stride;  // bytes between rows on the row side
+  FastDiv div_n;      // stick index -> (y, x)
+  uint32_t tc_shift;  // log2(T / 8): 1 KiB chunks per row
+};
+constexpr int kSmallLdsB = 1024 * 128 + 32 * 128;  // n rows of T sticks + 128 B each, or n T dense sticks
+
+template <bool R2D, int NL, bool POW2>
+__global__ __launch_bounds__(kThreads) void dma_stick_small_kernel(const char* __restrict__ src_arg,
+                                                                   char* __restrict__ dst_arg, StepNest<NL> nst,
+                                                                   SmallTile st) {
+  __shared__ __align__(16) char lds[kSmallLdsB];
+  const char* src = src_arg;
+  char* dst = dst_arg;
+  const StepNest<NL> x = read_step(nst, src, dst);
+  const uint32_t n = pinned(st.n), T = pinned(st.T), r_stride = pinned(st.r_stride), tcs = pinned(st.tc_shift);
+  const FastDiv dn{pinned(st.div_n.d), pinned(st.div_n.mul), pinned(st.div_n.shift)};
+  uint32_t so, sd;
+  step_offsets<NL, POW2>(x, blockIdx.x, so, sd);
+  const Rsrc rs = make_rsrc(src, x.span_s), rd = make_rsrc(dst, x.span_d);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t lane = threadIdx.x % 64, v = lane * 16;
+  const uint32_t chunks = n * T / 8;  // 1 KiB chunks per tile
+  const uint32_t row_b = T * 128 + 128;  // R2D: a padded LDS row
+  const uint32_t tc = T / 8;            // chunks per row (1 << tcs)
+  constexpr int kMaxPer = 1024 / 8 / 4;  // chunks per wavefront at most
+  // Loads: R2D, chunk c = sticks 8 (c % tc) .. + 7 of row c / tc into its
+  // LDS row; D2R, dense chunk c into LDS as it lies.
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    const uint32_t c = 4 * k + wave;
+    if (c >= chunks) break;
+    if constexpr (R2D) {
+      const uint32_t r = c >> tcs, cy = c & (tc - 1);
+      load_lds16(rs, v, so + r * r_stride + cy * 1024, lds + r * row_b + cy * 1024);
+    } else {
+      load_lds16(rs, v, so + c * 1024, lds + c * 1024);
+    }
+  }
+  wait_loads();
+  __syncthreads();
+  // Stores: R2D, dense chunk m (sticks 8m .. 8m + 7, stick s = (y, x) =
+  // (s / n, s % n)) from the LDS rows; D2R, chunk m = sticks 8 (m % tc) ..
+  // + 7 of row m / tc from the dense LDS block.
+  u32x4 r[kMaxPer];
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    const uint32_t m = 4 * k + wave;
+    if (m >= chunks) break;
+    if constexpr (R2D) {
+      const uint32_t s = 8 * m + lane / 8, y = fdiv(s, dn), xr = s - y * n;
+      r[k] = *reinterpret_cast<const u32x4*>(lds + xr * row_b + y * 128 + (lane % 8) * 16);
+    } else {
+      const uint32_t row = m >> tcs, y = (m & (tc - 1)) * 8 + lane / 8;
+      r[k] = *reinterpret_cast<const u32x4*>(lds + (y * n + row) * 128 + (lane % 8) * 16);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    const uint32_t m = 4 * k + wave;
+    if (m >= chunks) break;
+    if constexpr (R2D)
+      store16(rd, v, sd + m * 1024, r[k]);
+    else
+      store16(rd, v, sd + (m >> tcs) * r_stride + (m & (tc - 1)) * 1024, r[k]);
+  }
+}
+
+// Compute units of the current device, cached per device; 0 if the runtime
+// cannot say.
+int dma_device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 0;
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 // Transpose nest: loop A is unit-stride in src, loop B unit-stride in dst.
@@ -986,6 +1075,64 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
           else
             dma_stick_tile_kernel<32, 32, false, false><<<grid, kThreads, 0, st>>>(src, dst, n);
           return check_launch("dma_stick_tile_kernel");
+        }
+      }
+      // A small side (n < 32 sticks, no multiple of 8: a batch of 3 beside
+      // the stick) whose other side is dense over both loops: n runs of T
+      // sticks against one dense run per tile (dma_stick_small_kernel).
+      const bool small_a = ai >= 0 && bi >= 0 && outer[ai].size < kTileSticks && outer[ai].size % 8 != 0 &&
+                           outer[bi].sd == outer[ai].size * row;
+      const bool small_b = !small_a && ai >= 0 && bi >= 0 && outer[bi].size < kTileSticks &&
+                           outer[bi].size % 8 != 0 && outer[ai].ss == outer[bi].size * row;
+      if (small_a || small_b) {
+        const int64_t ns = small_a ? outer[ai].size : outer[bi].size;    // rows
+        const int64_t nl = small_a ? outer[bi].size : outer[ai].size;    // sticks along a row
+        const int64_t rs = small_a ? outer[ai].ss : outer[bi].sd;        // row stride, row side
+        int64_t T = 8;
+        while (ns * T * 2 <= 1024 && nl % (T * 2) == 0) T *= 2;
+        // Smaller tiles while the grid would leave compute units idle (a
+        // 16 MiB tensor in 128 KiB tiles fills half the device).
+        int64_t others = 1;
+        for (size_t k = 0; k < outer.size(); ++k)
+          if (static_cast<int>(k) != ai && static_cast<int>(k) != bi) others *= outer[k].size;
+        const int64_t cus = dma_device_cus() > 0 ? dma_device_cus() : 256;
+        while (T > 8 && nl / T * others < cus) T /= 2;
+        std::vector<Loop> tl;
+        if (nl / T > 1) tl.push_back({nl / T, small_a ? T * row : ns * T * row, small_a ? ns * T * row : T * row});
+        int64_t tiles = nl / T;
+        for (size_t k = 0; k < outer.size(); ++k) {
+          if (static_cast<int>(k) == ai || static_cast<int>(k) == bi) continue;
+          tl.push_back(outer[k]);
+          tiles *= outer[k].size;
+        }
+        const int64_t tile_s = small_a ? (ns - 1) * rs + T * row : ns * T * row;
+        const int64_t tile_d = small_a ? ns * T * row : (ns - 1) * rs + T * row;
+        const StepSpan sp = step_span(tl, off_s, off_d, tile_s, tile_d);
+        if (nl % T == 0 && sp.ok && rs > 0 && tiles < (int64_t{1} << 31)) {
+          uint32_t tcs = 0;
+          while ((int64_t{8} << tcs) < T) ++tcs;
+          const SmallTile smt{static_cast<uint32_t>(ns), static_cast<uint32_t>(T), static_cast<uint32_t>(rs),
+                              make_fastdiv(static_cast<uint32_t>(ns)), tcs};
+          const dim3 grid(static_cast<uint32_t>(tiles));
+          auto small_go = [&](auto nl_c) {
+            constexpr int NL = decltype(nl_c)::value;
+            const StepNest<NL> x = make_step<NL>(tl, tiles, off_s, off_d, sp.span_s, sp.span_d, 0, 0);
+            if (small_a && sp.pow2)
+              dma_stick_small_kernel<true, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x, smt);
+            else if (small_a)
+              dma_stick_small_kernel<true, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x, smt);
+            else if (sp.pow2)
+              dma_stick_small_kernel<false, NL, true><<<grid, kThreads, 0, st>>>(src, dst, x, smt);
+            else
+              dma_stick_small_kernel<false, NL, false><<<grid, kThreads, 0, st>>>(src, dst, x, smt);
+          };
+          switch (tl.size()) {
+            case 1: small_go(std::integral_constant<int, 1>{}); break;
+            case 2: small_go(std::integral_constant<int, 2>{}); break;
+            case 3: small_go(std::integral_constant<int, 3>{}); break;
+            default: small_go(std::integral_constant<int, 4>{}); break;
+          }
+          return check_launch("dma_stick_small_kernel");
         }
       }
     }
