@@ -659,3 +659,69 @@ def test_key_stride_near_the_descriptor_limit(cuda, Sq):
     assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
     del k, v, kv
     torch.cuda.empty_cache()
+
+
+# Decode calls whose (sequence, KV head, chunk) grid fills the device stream
+# dense K / V through the split-KV decode kernels: one chunk per sequence, or
+# several and the merge pass; a ragged last 64-token run; g = 1 and 16; K / V
+# rows padded past D.
+DENSE_DECODE_CASES = [
+    (32, 32, 8, 4096, 0),  # Llama-3-8B decode: one chunk per (sequence, KV head)
+    (4, 32, 8, 32768, 0),  # long context: 8 chunks and the merge pass
+    (2, 16, 8, 20037, 0),  # 16 chunks, the last run 5 tokens
+    (64, 64, 64, 1000, 0),  # g = 1, a ragged last run
+    (16, 256, 16, 2049, 64),  # g = 16, K / V rows 192 features apart
+    (256, 32, 8, 70, 0),  # shorter than one wavefront's share
+]
+
+
+def _dense_case(cuda, B, Hq, Hkv, Skv, pad, seed):
+    D = 128
+    q = randn((B, Hq, 1, D), seed)
+    kf, vf = randn((B, Hkv, Skv, D + pad), seed + 1), randn((B, Hkv, Skv, D + pad), seed + 2)
+    k, v = kf.to(cuda)[..., :D], vf.to(cuda)[..., :D]  # views with the padded token stride
+    assert k.stride(2) == D + pad
+    return q, k, v, kf[..., :D], vf[..., :D]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad", DENSE_DECODE_CASES, ids=str)
+def test_dense_decode_through_split_kernels(cuda, B, Hq, Hkv, Skv, pad):
+    """Every sequence against CPU fp32 SDPA; LSE against the fp64
+    logsumexp within 1e-4, below ln(n / (n - 1)) for these contexts' equal
+    scores, the shift of one lost or doubled key."""
+    q, k, v, kc, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, SEED + 110 + Skv)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    out = out.cpu()
+    for b in range(B):
+        assert_close(out[b:b + 1], OA.sdpa_cpu_fp32(q[b:b + 1], kc[b:b + 1], vc[b:b + 1]))
+    lse64 = np.stack([OA.decode_lse_fp64(q[b, :, 0].numpy(), kc[b].numpy()) for b in range(B)])
+    err = np.abs(lse.cpu().double().numpy()[..., 0] - lse64).max()
+    assert err <= 1e-4, err
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad", [DENSE_DECODE_CASES[1], DENSE_DECODE_CASES[2], DENSE_DECODE_CASES[4]],
+                         ids=str)
+def test_dense_decode_counts_every_key_once(cuda, B, Hq, Hkv, Skv, pad):
+    """q = 0: every score is 0, so LSE = ln(Skv) up to the fp32 rounding of
+    the log (a lost or doubled key moves it by at least 1/Skv) and out is the
+    mean of V over the keys."""
+    q, k, v, _, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, SEED + 120 + Skv)
+    out, lse = run(cuda, torch.zeros_like(q), k, v, enable_gqa=True, return_lse=True)
+    assert np.abs(lse.cpu().double().numpy() - math.log(Skv)).max() <= 4e-6
+    g = Hq // Hkv
+    assert_close(out, vc.float().mean(dim=2, keepdim=True).repeat_interleave(g, dim=1))
+
+
+def test_dense_decode_keys_expanded_along_the_sequence(cuda):
+    """K and V expanded from one row (token stride 0) on a grid the
+    split-KV kernels take: each row's output is that value row and its LSE
+    scale q.k + ln(Skv)."""
+    B, Hq, Hkv, Skv, D = 32, 32, 8, 4096, 128
+    q = randn((B, Hq, 1, D), SEED + 130)
+    k1, v1 = randn((B, Hkv, 1, D), SEED + 131), randn((B, Hkv, 1, D), SEED + 132)
+    k, v = k1.to(cuda).expand(B, Hkv, Skv, D), v1.to(cuda).expand(B, Hkv, Skv, D)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    g = Hq // Hkv
+    assert_close(out, v1.float().repeat_interleave(g, dim=1))
+    s = (q.double() @ k1.double().repeat_interleave(g, dim=1).transpose(-1, -2))[..., 0, 0] / math.sqrt(D)
+    assert np.allclose(lse.cpu().double().numpy()[..., 0], (s + math.log(Skv)).numpy(), atol=1e-4, rtol=0)

@@ -46,6 +46,7 @@
 #include <cmath>
 #include <mutex>
 
+#include "decode_dense.h"
 #include "spyre_common.h"
 
 namespace {
@@ -86,6 +87,10 @@ struct SplitArgs {
   int64_t num_pages;
   int B, Hq, Hkv, g, max_chunks, chunk_pages, max_ctx;
   float scale_log2;
+  // Dense K / V (decode_dense_kernel): [B, Hkv, S, D] with feature stride 1
+  // and these strides (elements), every sequence max_ctx tokens long; q
+  // [B, Hq, D] with strides q_sb, q_sh.  block_table and ctx_lens unused.
+  int64_t q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
 };
 
 // Pages of a context and the number of chunks (of at most chunk_pages
@@ -172,6 +177,16 @@ struct LoadOffsets {
     vx = (r * kPage + cx * 8) * 2;
     vy = ((8 + r) * kPage + cy * 8) * 2;
   }
+  // Dense K / V, tokens k_row / v_row bytes apart: the K loads as above;
+  // vx is the dense V load's offset (load_v_dense), vy unused.
+  __device__ __forceinline__ LoadOffsets(int lane, int k_row, int v_row) {
+    const int r = lane & 7, cx = chunk_x(lane), cy = chunk_y(lane);
+    const int tx = 8 * (r >> 2) + (r & 3);
+    kx = tx * k_row + cx * 16;
+    ky = (tx + 16) * k_row + cy * 16;
+    vx = 8 * (lane >> 4) * v_row + 16 * (lane & 15);
+    vy = 0;
+  }
 };
 
 // Raw K loads of one page: for block jh and stick tile t, X -> ka[jh][2t],
@@ -187,6 +202,50 @@ __device__ __forceinline__ void load_k(f16x8 (&ka)[4][D / 32], Rsrc kr, const Lo
       ka[jh][2 * t + 1] = bload(kr, lo.ky, so);
     }
   }
+}
+
+// Dense K: the same X / Y stick loads, tokens k_row bytes apart (the
+// token's two 128-byte sticks side by side instead of 8 KiB apart).
+template <int D>
+__device__ __forceinline__ void load_k_dense(f16x8 (&ka)[4][D / 32], Rsrc kr, int kx, int ky, int k_row) {
+#pragma unroll
+  for (int jh = 0; jh < 4; ++jh) {
+#pragma unroll
+    for (int t = 0; t < D / 64; ++t) {
+      const int so = (32 * (jh >> 1) + 4 * (jh & 1)) * k_row + t * 128;
+      ka[jh][2 * t] = bload(kr, kx, so);
+      ka[jh][2 * t + 1] = bload(kr, ky, so);
+    }
+  }
+}
+
+// Dense V ([tokens, D], tokens v_row bytes apart): lane l = (feature block
+// f = l & 15, token group tg = l >> 4) loads features 8f .. 8f + 7 of tokens
+// 32j + 8tg + i into va[i][j]; each instruction reads four whole 256-byte
+// token rows.  transposed_col turns a j's eight registers into the PV
+// operands (D = 128 only: sixteen feature blocks fill the MFMA's rows).
+template <int D>
+__device__ __forceinline__ void load_v_dense(f16x8 (&va)[D / 16][2], Rsrc vr, int vo, int v_row) {
+  static_assert(D == 128, "the dense V operand takes 16 feature blocks");
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) va[i][j] = bload(vr, vo, (32 * j + i) * v_row);
+}
+
+// Column a of the 8 x 8 block of 16-bit elements va[0..7][j]: element i is
+// va[i][j][a] (feature 8f + a of token 32j + 8tg + i, for the loads above).
+template <int D>
+__device__ __forceinline__ f16x8 transposed_col(const f16x8 (&va)[D / 16][2], int j, int a) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 x;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t lo = __builtin_bit_cast(u32x4, va[2 * p][j])[a / 2];
+    const uint32_t hi = __builtin_bit_cast(u32x4, va[2 * p + 1][j])[a / 2];
+    x[p] = (a & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+  }
+  return __builtin_bit_cast(f16x8, x);
 }
 
 // Raw V^T loads of one page: for d block db, X (d rows 16db + 0..7) ->
@@ -209,7 +268,10 @@ __device__ __forceinline__ void load_v(f16x8 (&va)[D / 16][2], Rsrc vr, const Lo
 // (head col, group grp) holds O^T[d = 16db + 4grp + v][col] unnormalised in
 // o[db][v], the running max m (log2 domain) and the row sum l of head col.
 // n_it = 0 leaves the empty partial (0, -inf, 0).
-template <int D>
+// DENSE: "pages" are 64-token runs of dense K / V (SplitArgs' dense
+// strides); lane (col, grp) then holds O^T[d = 8 (4 grp + v) + db][col] in
+// o[db][v] (the PV rows are features 8i + db, see transposed_col).
+template <int D, bool DENSE = false>
 __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh, int p0, int n_it,
                                              int ctx, int lane, f32x4 (&o)[D / 16], float& m_out,
                                              float& l_out) {
@@ -221,15 +283,16 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   l_out = 0.f;
   if (n_it <= 0) return;
   const int col = lane & 15, grp = lane >> 4;
-  const int32_t* trow = a.block_table + static_cast<int64_t>(b) * a.bt_stride + p0;
+  const int32_t* trow = DENSE ? nullptr : a.block_table + static_cast<int64_t>(b) * a.bt_stride + p0;
   // One lane per page: the page ids of the next 64 pages.
-  int ids = lane < n_it ? trow[lane] : 0;
+  int ids = !DENSE && lane < n_it ? trow[lane] : 0;
 
   // Q^T operand: lane = (head col, d group grp); padded heads are zero.
   f16x8 qb[DS];
   {
     const bool ok = col < a.g;
-    const _Float16* qr = a.q + (static_cast<int64_t>(b) * a.Hq + kvh * a.g + (ok ? col : 0)) * D;
+    const int h = kvh * a.g + (ok ? col : 0);
+    const _Float16* qr = DENSE ? a.q + b * a.q_sb + h * a.q_sh : a.q + (static_cast<int64_t>(b) * a.Hq + h) * D;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
       f16x8 x = *reinterpret_cast<const f16x8*>(qr + 32 * ds + 8 * grp);
@@ -244,21 +307,37 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 
   // Page it's K/V resources (page id broadcast from lane it % 64).
   const int head_bytes = static_cast<int>(head_elems * 2);
+  // Dense: tokens 64 (p0 + it) .. + 63 of the sequence's K / V head, the
+  // range ending with the last token (the host keeps a 64-token run of
+  // either within 2^30 bytes, so no per-lane offset wraps).
+  const int k_row = DENSE ? static_cast<int>(a.k_ss * 2) : 0, v_row = DENSE ? static_cast<int>(a.v_ss * 2) : 0;
   auto locate = [&](int it, Rsrc& kr, Rsrc& vr) {
-    int64_t phys = __builtin_amdgcn_readlane(ids, it & 63);
-    const bool bad = phys < 0 || phys >= a.num_pages;
-    poisoned |= bad;
-    if (bad) phys = 0;  // stay in bounds; the result is poisoned below
-    kr = page_rsrc(a.k + phys * page_elems + kvh * head_elems, head_bytes);
-    vr = page_rsrc(a.v + phys * page_elems + kvh * head_elems, head_bytes);
+    if constexpr (DENSE) {
+      const int t0 = (p0 + it) * kPage, rows = min(kPage, ctx - t0);
+      kr = page_rsrc(a.k + b * a.k_sb + kvh * a.k_sh + t0 * a.k_ss, (rows - 1) * k_row + 2 * D);
+      vr = page_rsrc(a.v + b * a.v_sb + kvh * a.v_sh + t0 * a.v_ss, (rows - 1) * v_row + 2 * D);
+    } else {
+      int64_t phys = __builtin_amdgcn_readlane(ids, it & 63);
+      const bool bad = phys < 0 || phys >= a.num_pages;
+      poisoned |= bad;
+      if (bad) phys = 0;  // stay in bounds; the result is poisoned below
+      kr = page_rsrc(a.k + phys * page_elems + kvh * head_elems, head_bytes);
+      vr = page_rsrc(a.v + phys * page_elems + kvh * head_elems, head_bytes);
+    }
   };
-  const LoadOffsets lo(lane);
+  const LoadOffsets lo = DENSE ? LoadOffsets(lane, k_row, v_row) : LoadOffsets(lane);
+  auto issue_k = [&](f16x8 (&ka)[4][DS], Rsrc kr) {
+    if constexpr (DENSE) load_k_dense<D>(ka, kr, lo.kx, lo.ky, k_row); else load_k<D>(ka, kr, lo);
+  };
+  auto issue_v = [&](f16x8 (&va)[DB][2], Rsrc vr) {
+    if constexpr (DENSE) load_v_dense<D>(va, vr, lo.vx, v_row); else load_v<D>(va, vr, lo);
+  };
   Rsrc kr, vr;
   locate(0, kr, vr);
   f16x8 ka[4][DS];
   f16x8 va[DB][2];
-  load_k<D>(ka, kr, lo);
-  load_v<D>(va, vr, lo);
+  issue_k(ka, kr);
+  issue_v(va, vr);
 
   for (int it = 0; it < n_it; ++it) {
     const int valid = min(kPage, ctx - (p0 + it) * kPage);
@@ -279,12 +358,12 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
     // they are in flight during this page's softmax and PV.
     const bool more = it + 1 < n_it;
     if (more) {
-      if (((it + 1) & 63) == 0) {
+      if (!DENSE && ((it + 1) & 63) == 0) {
         const int nx = it + 1 + lane;
         ids = nx < n_it ? trow[nx] : 0;
       }
       locate(it + 1, kr, vr);
-      load_k<D>(ka, kr, lo);
+      issue_k(ka, kr);
     }
 
     // This lane holds head col's scores for tokens 32j + 8grp + 4h + v.
@@ -316,25 +395,42 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
     m_run = m_new;
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] *= alpha;
+    if constexpr (DENSE) {
+      // va[i][j] holds token 32j + 8grp + i; past the context it may hold
+      // any bits (even NaN): zero it so that 0 * V stays 0.
+      if (valid < kPage) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db) shuffle_pair(va[db][0], va[db][1], bit3);
-    if (valid < kPage) {
-      // Tokens past the context may hold any bits (even NaN); zero them so
-      // that 0 * V stays 0 in the PV product.
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            if (32 * j + 8 * grp + i >= valid) va[i][j] = f16x8{};
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(transposed_col<D>(va, j, db), pb[j], o[db], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) shuffle_pair(va[db][0], va[db][1], bit3);
+      if (valid < kPage) {
+        // Tokens past the context may hold any bits (even NaN); zero them so
+        // that 0 * V stays 0 in the PV product.
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (32 * j + 8 * grp + e >= valid) va[db][j][e] = static_cast<_Float16>(0.f);
+      }
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (32 * j + 8 * grp + e >= valid) va[db][j][e] = static_cast<_Float16>(0.f);
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
     }
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
-    if (more) load_v<D>(va, vr, lo);
+    if (more) issue_v(va, vr);
   }
   if (poisoned) l_run = NAN;  // propagates to the merged output: NaN, not a fault
   l_run += wave_xor(l_run, 16);
@@ -348,11 +444,11 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 // and the whole workgroup writes the result: fp16 out and LSE when the
 // sequence has one chunk and out is given, else the chunk's partial (O per
 // q head and feature; m, l) into the workspace for the merge pass.
-template <int D>
+template <int D, bool DENSE = false>
 __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int kvh, int wave,
                                          int lane) {
   constexpr int DB = D / 16;
-  const int ctx_raw = a.ctx_lens[b];
+  const int ctx_raw = DENSE ? a.max_ctx : a.ctx_lens[b];
   const int ctx = min(max(ctx_raw, 0), a.max_ctx);
   const int n_pages = pages_of(ctx);
   const int nch = chunks_of(ctx, a.chunk_pages);
@@ -364,7 +460,7 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
   const int w1 = cp0 + static_cast<int>(static_cast<int64_t>(wave + 1) * nc / kWaves);
   f32x4 o[DB];
   float m, l;
-  stream_pages<D>(a, b, kvh, w0, w1 - w0, ctx, lane, o, m, l);
+  stream_pages<D, DENSE>(a, b, kvh, w0, w1 - w0, ctx, lane, o, m, l);
   // Every wavefront's partial goes to LDS once; then each thread folds
   // output elements over the kWaves partials, in wavefront order.  Lane
   // (col, grp) holds O^T[d = 16 db + 4 grp + v][col] in o[db][v]; a row of
@@ -392,7 +488,7 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
     const int r = e >> 2;
     const int col = r % a.g, r2 = r / a.g;
     const int grp = r2 & 3, db = r2 >> 2;
-    const int d = 16 * db + 4 * grp + v;
+    const int d = DENSE ? 8 * (4 * grp + v) + db : 16 * db + 4 * grp + v;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][col]);
@@ -486,9 +582,19 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_list_ker
   run_item<D>(a, lo, bs - __builtin_amdgcn_readfirstlane(s_pre[lo]), kvh, wave, lane);
 }
 
+// Dense decode: item x = ((b Hkv + kvh) max_chunks + c); every sequence has
+// max_chunks chunks of its max_ctx tokens (grid = B Hkv max_chunks).
+template <int D>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_dense_kernel(SplitArgs a) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int item = blockIdx.x;
+  const int c = item % a.max_chunks, r = item / a.max_chunks;
+  run_item<D, true>(a, r / a.Hkv, c, r % a.Hkv, wave, lane);
+}
+
 struct MergeArgs {
   const float* ws;
-  const int32_t* ctx_lens;
+  const int32_t* ctx_lens;  // null: every sequence max_ctx tokens (dense K / V)
   _Float16* out;
   float* lse;
   int B, Hq, Hkv, g, max_chunks, chunk_pages, max_ctx;
@@ -507,7 +613,7 @@ template <int D>
 __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int kvh = h / a.g, hh = h % a.g;
-  const int ctx_raw = a.ctx_lens[b];
+  const int ctx_raw = a.ctx_lens ? a.ctx_lens[b] : a.max_ctx;
   const int ctx = min(max(ctx_raw, 0), a.max_ctx);
   const int ns = chunks_of(ctx, a.chunk_pages);
   if (a.skip_single && ns == 1) return;
@@ -754,6 +860,75 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
   p.ma.skip_single = 1;
   return launch_merge(p, st);
 }
+
+// ------------------------------------------------ dense K / V (SDPA decode) --
+
+namespace spyre_hip {
+
+DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
+  DenseDecodePlan p;
+  if (D != 128 || B <= 0 || B > 65535 || Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > kCols || Skv <= 0) return p;
+  const int slots = split_slots(D) > 0 ? split_slots(D) : 256;
+  const int64_t pairs = static_cast<int64_t>(B) * Hkv;
+  // Tokens per wavefront: 512 (as the paged default), halved down to one
+  // page while the grid would leave workgroup slots empty.
+  int split = 512;
+  while (split > kPage && pairs * max_chunks_for(Skv, split) < slots) split /= 2;
+  const int64_t nc0 = max_chunks_for(Skv, split);
+  if (pairs * nc0 < slots || pairs * nc0 >= (int64_t{1} << 31)) return p;
+  p.chunk_pages = balanced_chunk_pages(pairs, Skv, kWaves * (split / kPage), slots);
+  p.chunks = chunks_of(Skv, p.chunk_pages);
+  p.ws_bytes = p.chunks > 1 ? static_cast<size_t>(pairs) * p.chunks * (Hq / Hkv) * (D + 2) * sizeof(float) : 0;
+  p.ok = true;
+  return p;
+}
+
+int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_t* q_strides, const void* k,
+                        const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out, float* lse,
+                        void* workspace, int B, int Hq, int Hkv, int Skv, int D, float scale, void* stream) {
+  SPYRE_REQUIRE(plan.ok && D == 128, SPYRE_EUNSUPPORTED, "dense decode: call not covered");
+  SPYRE_REQUIRE(plan.chunks == 1 || workspace, SPYRE_EINVAL, "dense decode: no workspace");
+  for (int i = 0; i < 3; ++i)
+    SPYRE_REQUIRE(k_strides[i] >= 0 && v_strides[i] >= 0, SPYRE_EUNSUPPORTED, "dense decode: negative stride");
+  SPYRE_REQUIRE(k_strides[2] < (int64_t{1} << 23) && v_strides[2] < (int64_t{1} << 23), SPYRE_EUNSUPPORTED,
+                "dense decode: token stride 2^23 elements or more");
+  SplitArgs sa{};
+  sa.q = static_cast<const _Float16*>(q);
+  sa.k = static_cast<const _Float16*>(k);
+  sa.v = static_cast<const _Float16*>(v);
+  sa.ws = static_cast<float*>(workspace);
+  sa.out = static_cast<_Float16*>(out);
+  sa.lse = lse;
+  sa.B = B;
+  sa.Hq = Hq;
+  sa.Hkv = Hkv;
+  sa.g = Hq / Hkv;
+  sa.max_chunks = plan.chunks;
+  sa.chunk_pages = plan.chunk_pages;
+  sa.max_ctx = Skv;
+  sa.scale_log2 = scale * kLog2e;
+  sa.q_sb = q_strides[0];
+  sa.q_sh = q_strides[1];
+  sa.k_sb = k_strides[0];
+  sa.k_sh = k_strides[1];
+  sa.k_ss = k_strides[2];
+  sa.v_sb = v_strides[0];
+  sa.v_sh = v_strides[1];
+  sa.v_ss = v_strides[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t items = static_cast<int64_t>(B) * Hkv * plan.chunks;
+  decode_dense_kernel<128><<<dim3(static_cast<unsigned>(items)), kThreads, 0, st>>>(sa);
+  hipError_t e = hipGetLastError();
+  SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode launch failed: %s", hipGetErrorString(e));
+  if (plan.chunks == 1) return SPYRE_OK;  // every workgroup wrote its sequence's output
+  const MergeArgs ma{sa.ws, nullptr, sa.out, lse, B, Hq, Hkv, sa.g, plan.chunks, plan.chunk_pages, Skv, 0};
+  decode_merge_kernel<128><<<dim3(Hq, B), 128, 0, st>>>(ma);
+  e = hipGetLastError();
+  SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode merge launch failed: %s", hipGetErrorString(e));
+  return SPYRE_OK;
+}
+
+}  // namespace spyre_hip
 
 // ------------------------------------------ the entry that allocates nothing --
 

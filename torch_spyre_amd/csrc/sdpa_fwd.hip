@@ -45,6 +45,7 @@
 #include <cmath>
 #include <type_traits>
 
+#include "decode_dense.h"
 #include "spyre_common.h"
 #include "transpose8.h"
 
@@ -1524,6 +1525,17 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
   return gp;
 }
 
+// Decode calls (one query per sequence, no mask, no causal flag) too large
+// for the short-decode kernel whose grid of (sequence, KV head, chunk) items
+// fills the device: they stream K / V through the split-KV decode kernels
+// (decode_attn.hip), whose operands come straight from memory into
+// registers -- no LDS tiles, no barrier per step.
+spyre_hip::DenseDecodePlan dense_route(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, int mask_kind) {
+  if (mask_kind != kNoMask || causal || Sq != 1) return {};
+  if (plan_grid(B, Hq, Hkv, Sq, Skv, D, false, SIZE_MAX).short_decode) return {};
+  return spyre_hip::dense_decode_plan(B, Hq, Hkv, Skv, D);
+}
+
 void launch_short(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
   const dim3 grid(f2.n_items);
   if (D == 128 && prescaled)
@@ -1688,8 +1700,11 @@ extern "C" size_t spyre_sdpa_fwd_call_workspace_bytes(const void* attn_mask, int
                                                       const int64_t* mask_strides, int B, int Hq, int Hkv,
                                                       int Sq, int Skv, int D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Sq < 0 || Skv < 0 || (D != 64 && D != 128)) return 0;
-  if (mask_kind == kNoMask)  // a key split's partials (calls without the causal flag)
-    return plan_grid(B, Hq, Hkv, Sq, Skv, D, false, SIZE_MAX).part_bytes;
+  if (mask_kind == kNoMask) {  // a key split's partials (calls without the causal flag)
+    const size_t split = plan_grid(B, Hq, Hkv, Sq, Skv, D, false, SIZE_MAX).part_bytes;
+    const spyre_hip::DenseDecodePlan dp = dense_route(B, Hq, Hkv, Sq, Skv, D, false, mask_kind);
+    return dp.ok ? std::max(split, dp.ws_bytes) : split;  // the split for calls the decode route refuses
+  }
   if (!mask_strides || mask_kind < kNoMask || mask_kind > kMaskBool) return 0;
   const MaskPlan mp = plan_mask(attn_mask, mask_kind, mask_strides, B, Hq, Sq, Skv);
   if (mp.route == kRouteCopied) return mp.copy_bytes;
@@ -1820,6 +1835,11 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
   fa.causal = is_causal ? 1 : 0;
   fa.scale_log2 = scale * kLog2e;
   if (lds_path) {
+    const spyre_hip::DenseDecodePlan dp = dense_route(B, Hq, Hkv, Sq, Skv, D, is_causal != 0, mask_kind);
+    if (dp.ok && k_strides[2] < (int64_t{1} << 23) && v_strides[2] < (int64_t{1} << 23) &&
+        (dp.ws_bytes == 0 || (workspace && aligned16(workspace) && workspace_bytes >= dp.ws_bytes)))
+      return spyre_hip::dense_decode_launch(dp, q, q_strides, k, k_strides, v, v_strides, out, lse, workspace, B,
+                                            Hq, Hkv, Skv, D, scale, stream);
     // K/V tiles (and mask blocks) shared through LDS.
     Fwd2Args f2{};
     f2.q = fa.q;
