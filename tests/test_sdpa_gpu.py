@@ -672,6 +672,8 @@ DENSE_DECODE_CASES = [
     (64, 64, 64, 1000, 0),  # g = 1, a ragged last run
     (16, 256, 16, 2049, 64),  # g = 16, K / V rows 192 features apart
     (256, 32, 8, 70, 0),  # shorter than one wavefront's share
+    (3, 32, 8, 4096, 0),  # 192 workgroups of one-page shares (three quarters of a 256-CU device)
+    (24, 32, 8, 520, 0),  # 192 single-chunk workgroups, a ragged last run
 ]
 
 

@@ -875,7 +875,10 @@ DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
   int split = 512;
   while (split > kPage && pairs * max_chunks_for(Skv, split) < slots) split /= 2;
   const int64_t nc0 = max_chunks_for(Skv, split);
-  if (pairs * nc0 < slots || pairs * nc0 >= (int64_t{1} << 31)) return p;
+  // At least half the slots busy: batch 3 x 4096 tokens (192 workgroups)
+  // 26.2 -> 15.1 us against the LDS kernel's key split, batch 24 x 512
+  // 27.8 -> 12.8 us.
+  if (2 * pairs * nc0 < slots || pairs * nc0 >= (int64_t{1} << 31)) return p;
   p.chunk_pages = balanced_chunk_pages(pairs, Skv, kWaves * (split / kPage), slots);
   p.chunks = chunks_of(Skv, p.chunk_pages);
   p.ws_bytes = p.chunks > 1 ? static_cast<size_t>(pairs) * p.chunks * (Hq / Hkv) * (D + 2) * sizeof(float) : 0;

@@ -1527,9 +1527,9 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
 
 // Decode calls (one query per sequence, no mask, no causal flag) too large
 // for the short-decode kernel whose grid of (sequence, KV head, chunk) items
-// fills the device: they stream K / V through the split-KV decode kernels
-// (decode_attn.hip), whose operands come straight from memory into
-// registers -- no LDS tiles, no barrier per step.
+// fills at least half the device: they stream K / V through the split-KV
+// decode kernels (decode_attn.hip), whose operands come straight from
+// memory into registers -- no LDS tiles, no barrier per step.
 spyre_hip::DenseDecodePlan dense_route(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, int mask_kind) {
   if (mask_kind != kNoMask || causal || Sq != 1) return {};
   if (plan_grid(B, Hq, Hkv, Sq, Skv, D, false, SIZE_MAX).short_decode) return {};
