@@ -202,6 +202,11 @@ def test_sdpa_call_workspace_routes(tsa):
     # (a grid of at most an eighth of the device splits down to one 64-key step per block)
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 16384, 128) == 32 * 32 * 130 * 4
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 40, 127, 64) == 0  # one step
+    # decode grids of at least half the device take the split-KV decode kernels on dense K / V:
+    # batch 32 x 4096 tokens is one chunk per (sequence, KV head), no partials; batch 2 x 20037
+    # tokens, 16 chunks of 20 pages each: [B, Hkv, 16, g, 128 + 2] fp32
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 32, 32, 8, 1, 4096, 128) == 0
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 2, 16, 8, 1, 20037, 128) == 2 * 8 * 16 * 2 * 130 * 4
     # staged as they lie: fp16 rows of 160 keys (320 B), bool rows of 160 B, broadcasts, wider rows
     assert need(1, [0, 0, 160, 1], 160) == 0
     assert need(3, [0, 0, 160, 1], 160) == 0
