@@ -100,22 +100,24 @@ def test_relayout_graph_replays_match_oracle(cuda):
         assert np.array_equal(got_t, OR.transpose_restick(bits).reshape(-1)), i
 
 
-def test_dense_decode_graph_replays_match_eager(cuda):
-    """A prepared batch-1 dense decode (SdpaCall: 32 key splits + merge) in
-    a graph; q and the newest key/value row rewritten eagerly before each
-    replay; every replay bit-equal to the eager call."""
+@pytest.mark.parametrize("B,S", [(1, 4096), (4, 8192)])
+def test_dense_decode_graph_replays_match_eager(cuda, B, S):
+    """A prepared dense decode in a graph -- batch 1 (short-decode kernel,
+    key splits + merge) and batch 4 x 8192 tokens (the split-KV decode
+    kernels, 8 chunks + merge); q and the newest key/value row rewritten
+    eagerly before each replay; every replay bit-equal to the eager call."""
     import torch_spyre_amd as tsa
 
     gg = torch.Generator(device=cuda).manual_seed(SEED + 95)
-    q = torch.randn((1, 32, 1, 128), generator=gg, device=cuda).half()
-    k = torch.randn((1, 8, 4096, 128), generator=gg, device=cuda).half()
-    v = torch.randn((1, 8, 4096, 128), generator=gg, device=cuda).half()
+    q = torch.randn((B, 32, 1, 128), generator=gg, device=cuda).half()
+    k = torch.randn((B, 8, S, 128), generator=gg, device=cuda).half()
+    v = torch.randn((B, 8, S, 128), generator=gg, device=cuda).half()
     call = tsa.SdpaCall(q, k, v, enable_gqa=True, return_lse=True)
     g = _capture(cuda, call)
     for i in range(3):
         q.copy_(torch.randn(q.shape, generator=gg, device=cuda).half())
-        k[:, :, 4095].copy_(torch.randn((1, 8, 128), generator=gg, device=cuda).half())
-        v[:, :, 4095].copy_(torch.randn((1, 8, 128), generator=gg, device=cuda).half())
+        k[:, :, S - 1].copy_(torch.randn((B, 8, 128), generator=gg, device=cuda).half())
+        v[:, :, S - 1].copy_(torch.randn((B, 8, 128), generator=gg, device=cuda).half())
         g.replay()
         want, want_lse = tsa.scaled_dot_product_attention(q, k, v, enable_gqa=True, return_lse=True)
         torch.cuda.synchronize()

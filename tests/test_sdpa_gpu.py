@@ -694,6 +694,7 @@ def test_dense_decode_through_split_kernels(cuda, B, Hq, Hkv, Skv, pad):
     q, k, v, kc, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, SEED + 110 + Skv)
     out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
     out = out.cpu()
+    assert torch.equal(run(cuda, q, k, v, enable_gqa=True).cpu(), out)  # without the LSE: the same bits
     for b in range(B):
         assert_close(out[b:b + 1], OA.sdpa_cpu_fp32(q[b:b + 1], kc[b:b + 1], vc[b:b + 1]))
     lse64 = np.stack([OA.decode_lse_fp64(q[b, :, 0].numpy(), kc[b].numpy()) for b in range(B)])
