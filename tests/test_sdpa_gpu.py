@@ -661,24 +661,26 @@ def test_key_stride_near_the_descriptor_limit(cuda, Sq):
     torch.cuda.empty_cache()
 
 
-# Decode calls whose (sequence, KV head, chunk) grid fills the device stream
-# dense K / V through the split-KV decode kernels: one chunk per sequence, or
-# several and the merge pass; a ragged last 64-token run; g = 1 and 16; K / V
-# rows padded past D.
+# Decode calls whose (sequence, KV head, chunk) grid fills at least half the
+# device stream dense K / V through the split-KV decode kernels: one chunk
+# per sequence, or several and the merge pass; a ragged last 64-token run;
+# g = 1 and 16; K / V rows padded past D; D = 128 and 64.
 DENSE_DECODE_CASES = [
-    (32, 32, 8, 4096, 0),  # Llama-3-8B decode: one chunk per (sequence, KV head)
-    (4, 32, 8, 32768, 0),  # long context: 8 chunks and the merge pass
-    (2, 16, 8, 20037, 0),  # 16 chunks, the last run 5 tokens
-    (64, 64, 64, 1000, 0),  # g = 1, a ragged last run
-    (16, 256, 16, 2049, 64),  # g = 16, K / V rows 192 features apart
-    (256, 32, 8, 70, 0),  # shorter than one wavefront's share
-    (3, 32, 8, 4096, 0),  # 192 workgroups of one-page shares (three quarters of a 256-CU device)
-    (24, 32, 8, 520, 0),  # 192 single-chunk workgroups, a ragged last run
+    (32, 32, 8, 4096, 0, 128),  # Llama-3-8B decode: one chunk per (sequence, KV head)
+    (4, 32, 8, 32768, 0, 128),  # long context: 8 chunks and the merge pass
+    (2, 16, 8, 20037, 0, 128),  # 16 chunks, the last run 5 tokens
+    (64, 64, 64, 1000, 0, 128),  # g = 1, a ragged last run
+    (16, 256, 16, 2049, 64, 128),  # g = 16, K / V rows 192 features apart
+    (256, 32, 8, 70, 0, 128),  # shorter than one wavefront's share
+    (3, 32, 8, 4096, 0, 128),  # 192 workgroups of one-page shares (three quarters of a 256-CU device)
+    (24, 32, 8, 520, 0, 128),  # 192 single-chunk workgroups, a ragged last run
+    (32, 32, 8, 4096, 0, 64),  # D = 64
+    (8, 32, 8, 16384, 0, 64),  # D = 64, chunks and the merge pass
+    (32, 16, 16, 2047, 8, 64),  # D = 64, g = 1, K / V rows 72 features apart, a ragged last run
 ]
 
 
-def _dense_case(cuda, B, Hq, Hkv, Skv, pad, seed):
-    D = 128
+def _dense_case(cuda, B, Hq, Hkv, Skv, pad, D, seed):
     q = randn((B, Hq, 1, D), seed)
     kf, vf = randn((B, Hkv, Skv, D + pad), seed + 1), randn((B, Hkv, Skv, D + pad), seed + 2)
     k, v = kf.to(cuda)[..., :D], vf.to(cuda)[..., :D]  # views with the padded token stride
@@ -686,12 +688,12 @@ def _dense_case(cuda, B, Hq, Hkv, Skv, pad, seed):
     return q, k, v, kf[..., :D], vf[..., :D]
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad", DENSE_DECODE_CASES, ids=str)
-def test_dense_decode_through_split_kernels(cuda, B, Hq, Hkv, Skv, pad):
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad,D", DENSE_DECODE_CASES, ids=str)
+def test_dense_decode_through_split_kernels(cuda, B, Hq, Hkv, Skv, pad, D):
     """Every sequence against CPU fp32 SDPA; LSE against the fp64
     logsumexp within 1e-4, below ln(n / (n - 1)) for these contexts' equal
     scores, the shift of one lost or doubled key."""
-    q, k, v, kc, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, SEED + 110 + Skv)
+    q, k, v, kc, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, D, SEED + 110 + Skv)
     out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
     out = out.cpu()
     assert torch.equal(run(cuda, q, k, v, enable_gqa=True).cpu(), out)  # without the LSE: the same bits
@@ -702,13 +704,12 @@ def test_dense_decode_through_split_kernels(cuda, B, Hq, Hkv, Skv, pad):
     assert err <= 1e-4, err
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad", [DENSE_DECODE_CASES[1], DENSE_DECODE_CASES[2], DENSE_DECODE_CASES[4]],
-                         ids=str)
-def test_dense_decode_counts_every_key_once(cuda, B, Hq, Hkv, Skv, pad):
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad,D", [DENSE_DECODE_CASES[i] for i in (1, 2, 4, 9, 10)], ids=str)
+def test_dense_decode_counts_every_key_once(cuda, B, Hq, Hkv, Skv, pad, D):
     """q = 0: every score is 0, so LSE = ln(Skv) up to the fp32 rounding of
     the log (a lost or doubled key moves it by at least 1/Skv) and out is the
     mean of V over the keys."""
-    q, k, v, _, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, SEED + 120 + Skv)
+    q, k, v, _, vc = _dense_case(cuda, B, Hq, Hkv, Skv, pad, D, SEED + 120 + Skv)
     out, lse = run(cuda, torch.zeros_like(q), k, v, enable_gqa=True, return_lse=True)
     assert np.abs(lse.cpu().double().numpy() - math.log(Skv)).max() <= 4e-6
     g = Hq // Hkv

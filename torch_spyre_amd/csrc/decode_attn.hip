@@ -177,14 +177,16 @@ struct LoadOffsets {
     vx = (r * kPage + cx * 8) * 2;
     vy = ((8 + r) * kPage + cy * 8) * 2;
   }
-  // Dense K / V, tokens k_row / v_row bytes apart: the K loads as above;
-  // vx is the dense V load's offset (load_v_dense), vy unused.
-  __device__ __forceinline__ LoadOffsets(int lane, int k_row, int v_row) {
+  // Dense K / V (head_dim d), tokens k_row / v_row bytes apart: the K
+  // loads as above; vx is the dense V load's offset (load_v_dense), vy
+  // unused.
+  __device__ __forceinline__ LoadOffsets(int lane, int k_row, int v_row, int d) {
     const int r = lane & 7, cx = chunk_x(lane), cy = chunk_y(lane);
     const int tx = 8 * (r >> 2) + (r & 3);
     kx = tx * k_row + cx * 16;
     ky = (tx + 16) * k_row + cy * 16;
-    vx = 8 * (lane >> 4) * v_row + 16 * (lane & 15);
+    const int fo = d == 128 ? 16 * (lane & 15) : 16 * (lane & 7) + 8 * ((lane >> 3) & 1);
+    vx = 8 * (lane >> 4) * v_row + fo;
     vy = 0;
   }
 };
@@ -219,14 +221,15 @@ __device__ __forceinline__ void load_k_dense(f16x8 (&ka)[4][D / 32], Rsrc kr, in
   }
 }
 
-// Dense V ([tokens, D], tokens v_row bytes apart): lane l = (feature block
-// f = l & 15, token group tg = l >> 4) loads features 8f .. 8f + 7 of tokens
-// 32j + 8tg + i into va[i][j]; each instruction reads four whole 256-byte
-// token rows.  transposed_col turns a j's eight registers into the PV
-// operands (D = 128 only: sixteen feature blocks fill the MFMA's rows).
-template <int D>
-__device__ __forceinline__ void load_v_dense(f16x8 (&va)[D / 16][2], Rsrc vr, int vo, int v_row) {
-  static_assert(D == 128, "the dense V operand takes 16 feature blocks");
+// Dense V ([tokens, D], tokens v_row bytes apart): lane l (token group tg =
+// l >> 4) loads 8 features of tokens 32j + 8tg + i into va[i][j], each
+// instruction four whole token rows.  D = 128: features 8f .. 8f + 7, f =
+// l & 15.  D = 64: features 8f + 4h .. + 7, f = l & 7, h = (l >> 3) & 1 (the
+// lanes of h = 1 start half a block on, and their last four features, past
+// the block, are never used).  transposed_col turns a j's eight registers
+// into the PV operands: MFMA db's row i is feature 8i + db (D = 128), or
+// 8 (i & 7) + 4 (i >> 3) + db (D = 64, db < 4).
+__device__ __forceinline__ void load_v_dense(f16x8 (&va)[8][2], Rsrc vr, int vo, int v_row) {
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -234,9 +237,8 @@ __device__ __forceinline__ void load_v_dense(f16x8 (&va)[D / 16][2], Rsrc vr, in
 }
 
 // Column a of the 8 x 8 block of 16-bit elements va[0..7][j]: element i is
-// va[i][j][a] (feature 8f + a of token 32j + 8tg + i, for the loads above).
-template <int D>
-__device__ __forceinline__ f16x8 transposed_col(const f16x8 (&va)[D / 16][2], int j, int a) {
+// va[i][j][a] (the a-th loaded feature of token 32j + 8tg + i).
+__device__ __forceinline__ f16x8 transposed_col(const f16x8 (&va)[8][2], int j, int a) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   u32x4 x;
 #pragma unroll
@@ -269,8 +271,8 @@ __device__ __forceinline__ void load_v(f16x8 (&va)[D / 16][2], Rsrc vr, const Lo
 // o[db][v], the running max m (log2 domain) and the row sum l of head col.
 // n_it = 0 leaves the empty partial (0, -inf, 0).
 // DENSE: "pages" are 64-token runs of dense K / V (SplitArgs' dense
-// strides); lane (col, grp) then holds O^T[d = 8 (4 grp + v) + db][col] in
-// o[db][v] (the PV rows are features 8i + db, see transposed_col).
+// strides); lane (col, grp) then holds O^T[d][col] in o[db][v] for d the
+// feature of PV row i = 4 grp + v of MFMA db (load_v_dense).
 template <int D, bool DENSE = false>
 __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh, int p0, int n_it,
                                              int ctx, int lane, f32x4 (&o)[D / 16], float& m_out,
@@ -325,17 +327,18 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
       vr = page_rsrc(a.v + phys * page_elems + kvh * head_elems, head_bytes);
     }
   };
-  const LoadOffsets lo = DENSE ? LoadOffsets(lane, k_row, v_row) : LoadOffsets(lane);
+  const LoadOffsets lo = DENSE ? LoadOffsets(lane, k_row, v_row, D) : LoadOffsets(lane);
   auto issue_k = [&](f16x8 (&ka)[4][DS], Rsrc kr) {
     if constexpr (DENSE) load_k_dense<D>(ka, kr, lo.kx, lo.ky, k_row); else load_k<D>(ka, kr, lo);
   };
-  auto issue_v = [&](f16x8 (&va)[DB][2], Rsrc vr) {
-    if constexpr (DENSE) load_v_dense<D>(va, vr, lo.vx, v_row); else load_v<D>(va, vr, lo);
+  constexpr int VR = DENSE ? 8 : DB;  // V registers per token half
+  auto issue_v = [&](f16x8 (&va)[VR][2], Rsrc vr) {
+    if constexpr (DENSE) load_v_dense(va, vr, lo.vx, v_row); else load_v<D>(va, vr, lo);
   };
   Rsrc kr, vr;
   locate(0, kr, vr);
   f16x8 ka[4][DS];
-  f16x8 va[DB][2];
+  f16x8 va[VR][2];
   issue_k(ka, kr);
   issue_v(va, vr);
 
@@ -409,7 +412,7 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(transposed_col<D>(va, j, db), pb[j], o[db], 0, 0, 0);
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(transposed_col(va, j, db), pb[j], o[db], 0, 0, 0);
     } else {
 #pragma unroll
       for (int db = 0; db < DB; ++db) shuffle_pair(va[db][0], va[db][1], bit3);
@@ -488,7 +491,8 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
     const int r = e >> 2;
     const int col = r % a.g, r2 = r / a.g;
     const int grp = r2 & 3, db = r2 >> 2;
-    const int d = DENSE ? 8 * (4 * grp + v) + db : 16 * db + 4 * grp + v;
+    const int i = 4 * grp + v;  // PV row
+    const int d = !DENSE ? 16 * db + i : D == 128 ? 8 * i + db : 8 * (i & 7) + 4 * (i >> 3) + db;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][col]);
@@ -867,7 +871,8 @@ namespace spyre_hip {
 
 DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
   DenseDecodePlan p;
-  if (D != 128 || B <= 0 || B > 65535 || Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > kCols || Skv <= 0) return p;
+  if ((D != 64 && D != 128) || B <= 0 || B > 65535 || Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > kCols || Skv <= 0)
+    return p;
   const int slots = split_slots(D) > 0 ? split_slots(D) : 256;
   const int64_t pairs = static_cast<int64_t>(B) * Hkv;
   // Tokens per wavefront: 512 (as the paged default), halved down to one
@@ -889,7 +894,7 @@ DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
 int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out, float* lse,
                         void* workspace, int B, int Hq, int Hkv, int Skv, int D, float scale, void* stream) {
-  SPYRE_REQUIRE(plan.ok && D == 128, SPYRE_EUNSUPPORTED, "dense decode: call not covered");
+  SPYRE_REQUIRE(plan.ok && (D == 64 || D == 128), SPYRE_EUNSUPPORTED, "dense decode: call not covered");
   SPYRE_REQUIRE(plan.chunks == 1 || workspace, SPYRE_EINVAL, "dense decode: no workspace");
   for (int i = 0; i < 3; ++i)
     SPYRE_REQUIRE(k_strides[i] >= 0 && v_strides[i] >= 0, SPYRE_EUNSUPPORTED, "dense decode: negative stride");
@@ -920,12 +925,18 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
   sa.v_ss = v_strides[2];
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(B) * Hkv * plan.chunks;
-  decode_dense_kernel<128><<<dim3(static_cast<unsigned>(items)), kThreads, 0, st>>>(sa);
+  if (D == 128)
+    decode_dense_kernel<128><<<dim3(static_cast<unsigned>(items)), kThreads, 0, st>>>(sa);
+  else
+    decode_dense_kernel<64><<<dim3(static_cast<unsigned>(items)), kThreads, 0, st>>>(sa);
   hipError_t e = hipGetLastError();
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode launch failed: %s", hipGetErrorString(e));
   if (plan.chunks == 1) return SPYRE_OK;  // every workgroup wrote its sequence's output
   const MergeArgs ma{sa.ws, nullptr, sa.out, lse, B, Hq, Hkv, sa.g, plan.chunks, plan.chunk_pages, Skv, 0};
-  decode_merge_kernel<128><<<dim3(Hq, B), 128, 0, st>>>(ma);
+  if (D == 128)
+    decode_merge_kernel<128><<<dim3(Hq, B), 128, 0, st>>>(ma);
+  else
+    decode_merge_kernel<64><<<dim3(Hq, B), 64, 0, st>>>(ma);
   e = hipGetLastError();
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode merge launch failed: %s", hipGetErrorString(e));
   return SPYRE_OK;

@@ -16,7 +16,7 @@ struct DenseDecodePlan {
 };
 
 // The plan for q [B, Hq, 1, D] against K / V of Skv tokens: covered when
-// D = 128, Hq / Hkv <= 16 and the (sequence, KV head, chunk) grid fills at
+// D in {64, 128}, Hq / Hkv <= 16 and the (sequence, KV head, chunk) grid fills at
 // least half of the device's workgroup slots (chunks of 8 wavefronts x
 // 64-512 tokens).
 DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D);
