@@ -729,3 +729,21 @@ def test_dense_decode_keys_expanded_along_the_sequence(cuda):
     assert_close(out, v1.float().repeat_interleave(g, dim=1))
     s = (q.double() @ k1.double().repeat_interleave(g, dim=1).transpose(-1, -2))[..., 0, 0] / math.sqrt(D)
     assert np.allclose(lse.cpu().double().numpy()[..., 0], (s + math.log(Skv)).numpy(), atol=1e-4, rtol=0)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D", [(1, 32, 8, 256, 4096, 128), (8, 32, 8, 64, 2048, 128),
+                                               (16, 32, 8, 16, 4096, 128), (1, 16, 4, 512, 4100, 64)], ids=str)
+def test_key_split_many_rows(cuda, B, Hq, Hkv, Sq, Skv, D):
+    """Chunked-prefill shapes whose blocks would not fill the device: the
+    keys are split and the partials of thousands of rows merged by the
+    kernel that gives each row its own threads; out against CPU fp32, LSE
+    against fp64."""
+    from torch_spyre_amd import _lib
+
+    assert _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, Sq, Skv, D) > 0  # split
+    q = randn((B, Hq, Sq, D), SEED + 140 + Sq)
+    k, v = randn((B, Hkv, Skv, D), SEED + 141), randn((B, Hkv, Skv, D), SEED + 142)
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
