@@ -174,8 +174,8 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
                                                "us_per_call_prepared": round(ms_p * 1e3, 2),
                                                "algorithmic_bytes": 1_050_624, "kernels_per_step": 1}
     # the Llama-3-8B decode step through SDPA with dense (unpaged) K/V:
-    # q [32, 32, 1, 128], k/v [32, 8, 4096, 128] (the q heads of a KV head
-    # packed into one block's rows)
+    # q [32, 32, 1, 128], k/v [32, 8, 4096, 128] (the split-KV decode kernel
+    # on the dense K / V: one workgroup per (sequence, KV head))
     q2 = torch.randn((32, HQ, 1, D), generator=gg, device=dev).half()
     k2 = torch.randn((32, HKV, 4096, D), generator=gg, device=dev).half()
     v2 = torch.randn((32, HKV, 4096, D), generator=gg, device=dev).half()
@@ -197,7 +197,7 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
                                               "us_per_call_prepared": round(ms_p * 1e3, 2), "kernels_per_step": 2}
     del q4, k4, v4
     # long-context decode through SDPA with dense K/V: q [4, 64, 1, 128],
-    # k/v [4, 8, 32768, 128] (keys split across blocks, partials merged)
+    # k/v [4, 8, 32768, 128] (8 chunks per (sequence, KV head), partials merged)
     q3 = torch.randn((4, 64, 1, D), generator=gg, device=dev).half()
     k3 = torch.randn((4, HKV, 32768, D), generator=gg, device=dev).half()
     v3 = torch.randn((4, HKV, 32768, D), generator=gg, device=dev).half()
@@ -210,6 +210,31 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
         "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
         "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb, "kernels_per_step": 2}
     del q3, k3, v3, ws3
+    # head_dim 64 decode through SDPA: q [32, 16, 1, 64], k/v [32, 16, 2048, 64]
+    # (two K/V sets, 537 MB, rotated)
+    q5 = torch.randn((32, 16, 1, 64), generator=gg, device=dev).half()
+    kv5 = [(torch.randn((32, 16, 2048, 64), generator=gg, device=dev).half(),
+            torch.randn((32, 16, 2048, 64), generator=gg, device=dev).half()) for _ in range(2)]
+    calls5 = [tsa.SdpaCall(q5, k, v) for k, v in kv5]
+    ms = timed(lambda i: calls5[i & 1](), steps, warmup, stream)
+    nb = 2 * kv5[0][0].numel() * 2 + 2 * q5.numel() * 2
+    res["dense_mha_decode_b32_h16_s2048_d64"] = {
+        "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+        "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb, "kernels_per_step": 1}
+    del q5, kv5, calls5
+    # chunked prefill: q [4, 32, 128, 128] against k/v [4, 8, 4096, 128] (keys split
+    # 8 ways so the blocks fill the device, partials merged)
+    q6 = torch.randn((4, HQ, 128, D), generator=gg, device=dev).half()
+    kv6 = [(torch.randn((4, HKV, 4096, D), generator=gg, device=dev).half(),
+            torch.randn((4, HKV, 4096, D), generator=gg, device=dev).half()) for _ in range(2)]
+    calls6 = [tsa.SdpaCall(q6, k, v, enable_gqa=True) for k, v in kv6]
+    ms = timed(lambda i: calls6[i & 1](), steps, max(warmup, 25), stream)  # MFMA work: past the clock settling
+    fl = 4.0 * 4 * HQ * 128 * 4096 * D
+    res["chunked_prefill_b4_h32_8_q128_k4096"] = {
+        "us_per_step": round(ms * 1e3, 2), "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 1),
+        "frac_of_f16_mfma_peak": round(fl / (ms * 1e-3) / 2.5e15, 4), "flops": fl,
+        "kernels_per_step": 2}
+    del q6, kv6, calls6
 
     def paged(lens, Hq, Hkv):
         pages = [(c + PAGE - 1) // PAGE for c in lens]
