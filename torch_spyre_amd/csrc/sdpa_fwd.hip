@@ -1506,13 +1506,15 @@ int device_cus();
 // grid gives every compute unit a block, each split at least 8 steps (512
 // keys; shorter splits lose more to the merge pass than they gain) -- or,
 // when the unsplit grid would use at most an eighth of the compute units,
-// at least one step (64 keys): such calls (batch-1 decode) are bound by
-// the latency of each block's chain of steps, not by the merge.
-// Returns nsplit; split_keys is a multiple of 64.
+// at least four steps (256 keys): such calls are bound by the latency of
+// each block's chain of steps more than by the merge (2 x 8 heads x 256
+// queries x 256 keys: 18.7 us split into 64-key runs, 15.6 unsplit or in
+// 256-key runs; 64 queries x 1024 keys: 12.7 split in 256-key runs, 14.3
+// unsplit).  Returns nsplit; split_keys is a multiple of 64.
 int plan_split(int64_t blocks, int Skv, int* split_keys) {
   *split_keys = Skv;
   const int64_t cus = device_cus() > 0 ? device_cus() : 256;
-  const int min_keys = blocks * 8 <= cus ? kKT : 512;
+  const int min_keys = blocks * 8 <= cus ? 4 * kKT : 512;
   if (blocks >= cus || Skv < 2 * min_keys) return 1;
   const int64_t ns = std::min<int64_t>((cus + blocks - 1) / blocks, Skv / min_keys);
   if (ns <= 1) return 1;
