@@ -747,3 +747,42 @@ def test_key_split_many_rows(cuda, B, Hq, Hkv, Sq, Skv, D):
     assert_close(out, OA.sdpa_cpu_fp32(q, k, v))
     _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
     assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
+def _route_shapes(n, seed):
+    """Seeded calls across the SDPA entry's routes -- short decode, the
+    split-KV decode kernels on dense K / V, the LDS kernel with and without
+    a key split (and its two merge kernels), causal -- with the CPU oracle's
+    work bounded: batch, q heads, KV heads, Sq, Skv, D, causal."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        D = int(rng.choice([64, 128]))
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        g = int(rng.choice([1, 2, 4, 8, 16]))
+        B = int(rng.choice([1, 2, 3, 5, 8, 16, 24, 32, 48]))
+        Sq = 1 if rng.random() < 0.5 else int(rng.choice([2, 7, 33, 64, 100, 256, 300]))
+        Skv = int(rng.integers(1, 9000))
+        causal = bool(Sq > 1 and rng.random() < 0.3)
+        if B * Hkv * g * Sq * Skv * D > 4e9 or B * Hkv * Skv * D > 6e7:
+            continue
+        out.append((B, Hkv * g, Hkv, Sq, Skv, D, causal))
+    return out
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Skv,D,causal", _route_shapes(24, SEED + 150), ids=str)
+def test_random_calls_across_routes(cuda, B, Hq, Hkv, Sq, Skv, D, causal):
+    """Out against CPU fp32 SDPA and LSE against the fp64 logsumexp for
+    seeded shapes that land on every route of the entry."""
+    q = randn((B, Hq, Sq, D), SEED + 151 + Skv)
+    k, v = randn((B, Hkv, Skv, D), SEED + 152), randn((B, Hkv, Skv, D), SEED + 153)
+    out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
+    out = out.cpu()
+    for b in range(B):
+        assert_close(out[b:b + 1], OA.sdpa_cpu_fp32(q[b:b + 1], k[b:b + 1], v[b:b + 1], is_causal=causal))
+    if Sq == 1:
+        lse64 = np.stack([OA.decode_lse_fp64(q[b, :, 0].numpy(), k[b].numpy()) for b in range(B)])[..., None]
+    else:
+        lse64 = np.concatenate([OA.sdpa_decomposition_fp64(q[b:b + 1], k[b:b + 1], v[b:b + 1], is_causal=causal,
+                                                           return_lse=True)[1] for b in range(B)])
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
