@@ -786,3 +786,21 @@ def test_random_calls_across_routes(cuda, B, Hq, Hkv, Sq, Skv, D, causal):
         lse64 = np.concatenate([OA.sdpa_decomposition_fp64(q[b:b + 1], k[b:b + 1], v[b:b + 1], is_causal=causal,
                                                            return_lse=True)[1] for b in range(B)])
     assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_dense_decode_ignores_rows_past_the_keys(cuda, D):
+    """K / V views of the first Skv rows of a larger cache whose later rows
+    hold NaN: a ragged last run must read nothing past row Skv - 1 (the
+    split-KV kernels' buffer range ends with the last key)."""
+    B, Hq, Hkv, Skv, Smax = 32, 32, 8, 2000, 2048
+    q = randn((B, Hq, 1, D), SEED + 160)
+    kf, vf = randn((B, Hkv, Smax, D), SEED + 161), randn((B, Hkv, Smax, D), SEED + 162)
+    kf[:, :, Skv:], vf[:, :, Skv:] = float("nan"), float("nan")
+    k, v = kf.to(cuda)[:, :, :Skv], vf.to(cuda)[:, :, :Skv]
+    out, lse = run(cuda, q, k, v, enable_gqa=True, return_lse=True)
+    kc, vc = kf[:, :, :Skv], vf[:, :, :Skv]
+    out = out.cpu()
+    for b in range(B):
+        assert_close(out[b:b + 1], OA.sdpa_cpu_fp32(q[b:b + 1], kc[b:b + 1], vc[b:b + 1]))
+    assert torch.isfinite(lse.cpu()).all()
