@@ -207,6 +207,9 @@ def test_sdpa_call_workspace_routes(tsa):
     # tokens, 16 chunks of 20 pages each: [B, Hkv, 16, g, 128 + 2] fp32
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 32, 32, 8, 1, 4096, 128) == 0
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 2, 16, 8, 1, 20037, 128) == 2 * 8 * 16 * 2 * 130 * 4
+    # D 64: batch 32 x 16 heads x 2048 tokens, one chunk; batch 8 x 16384 tokens, 4 chunks of 64 + 2
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 32, 16, 16, 1, 2048, 64) == 0
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 8, 32, 8, 1, 16384, 64) == 8 * 8 * 4 * 4 * 66 * 4
     # staged as they lie: fp16 rows of 160 keys (320 B), bool rows of 160 B, broadcasts, wider rows
     assert need(1, [0, 0, 160, 1], 160) == 0
     assert need(3, [0, 0, 160, 1], 160) == 0
