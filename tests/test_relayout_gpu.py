@@ -460,3 +460,36 @@ def test_small_side_stick_tiles_vs_oracle(cuda, sizes, pad):
     back = tsa.from_device_layout(dev)
     torch.cuda.synchronize()
     assert torch.equal(back.contiguous().view(torch.int16), x.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [[1000, 1000], [3, 64, 4100], [8, 1024, 512], [4096, 2048]], ids=str)
+def test_relayout_other_dtypes_vs_oracle(cuda, dtype, shape):
+    """fp32 tensors (32 elements a stick) and bf16 tensors (16-bit patterns
+    in the fp16 device format) to their default device layout and back: the
+    device bytes equal the oracle's DMA execution, the round trip is
+    bit-exact."""
+    import math
+
+    import torch_spyre_amd as tsa
+
+    gen = torch.Generator().manual_seed(SEED + 170 + len(shape))
+    n = math.prod(shape)
+    if dtype == torch.float32:
+        raw = torch.randint(-(2 ** 31), 2 ** 31 - 1, (n,), generator=gen, dtype=torch.int64).to(torch.int32)
+        name, npt = "float32", np.uint32
+    else:
+        raw = torch.randint(-(2 ** 15), 2 ** 15 - 1, (n,), generator=gen, dtype=torch.int32).to(torch.int16)
+        name, npt = "float16", np.uint16
+    x = raw.view(dtype).view(shape)
+    stl = tsa.SpyreTensorLayout(shape, dtype)
+    o = OL.stl_default(shape, name)
+    assert (stl.device_size, stl.stride_map) == (o.device_size, o.stride_map)
+    dev = tsa.to_device_layout(x.to(cuda), stl)
+    torch.cuda.synchronize()
+    got = tsa.device_buffer(dev).contiguous().view(raw.dtype).cpu().numpy().view(npt).reshape(-1)
+    want = OL.h2d(raw.numpy().view(npt), shape, OL.contiguous_strides(shape), 0, o)
+    assert got.size >= want.size
+    assert np.array_equal(got[:want.size], want)
+    back = dev.cpu()
+    assert torch.equal(back.view(raw.dtype).reshape(-1), raw)
