@@ -191,6 +191,20 @@ int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, const void* w
                                       int Hkv, int D, int max_context_len, int split_tokens,
                                       void* stream);
 
+/* Host-side check of the addresses the dense decode route (the SDPA entry's
+ * one-query calls on dense K / V, below) loads for one 64-token run of a
+ * K / V head of which `rows` tokens (1..64) exist, tokens k_row / v_row
+ * bytes apart: the largest byte end, from the run's first token, of any K
+ * load (k_end) and V load (v_end) that touches memory, and the number of
+ * such loads.  Computed from the same address functions as the kernel, on
+ * the CPU (no device is used).  The kernel's buffer ranges end at
+ * (rows - 1) * row + 2 * D bytes; a result beyond that would read past the
+ * view.  No reference counterpart (the reference has no device decode
+ * kernel; its decode SDPA is the decomposition of
+ * torch_spyre/_inductor/decompositions.py:523-609). */
+int spyre_dense_decode_load_extent(int D, int rows, int64_t k_row, int64_t v_row, int64_t* k_end,
+                                   int64_t* v_end, int64_t* n_loads);
+
 /* Bytes of the chunk-partial scratch that spyre_paged_decode_attn_noalloc_f16
  * keeps in the library (one copy per GPU, held until the process ends). */
 #define SPYRE_DECODE_SCRATCH_BYTES (16u << 20)

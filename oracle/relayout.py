@@ -13,7 +13,7 @@ For a row-major [R, C] tensor X (C, R multiples of 64 here):
                    (restickify target, torch_spyre/_inductor/pass_utils.py:749-781;
                    the dim_order=[1,0] weight layout, torch_spyre/model_utils.py:111-138)
 
-Parity pins (tests/test_oracle_relayout.py): each closed form equals the
+Parity pins (tests/test_oracle_layout.py): each closed form equals the
 generic DMA loop-nest execution of ``oracle.layout`` for the corresponding
 SpyreTensorLayout on several shapes, and the layouts themselves are pinned by
 the reference's golden tables.

@@ -175,6 +175,29 @@ def test_sdpa_override_mode(cuda):
     assert_close(got, OA.sdpa_cpu_fp32(q.cpu(), k.cpu(), v.cpu(), is_causal=True))
 
 
+def test_sdpa_override_leaves_other_shapes_to_torch(cuda):
+    """Calls torch serves but this library does not -- a value head dim
+    other than the query's, a key / value batch broadcast against the
+    query's -- run torch's own SDPA inside sdpa_override (no error, torch's
+    result)."""
+    import torch.nn.functional as F
+
+    import torch_spyre_amd as tsa
+
+    g = torch.Generator().manual_seed(SEED + 12)
+    q = torch.randn((2, 8, 16, 128), generator=g).half().to(cuda)
+    k = torch.randn((2, 8, 40, 128), generator=g).half().to(cuda)
+    v64 = torch.randn((2, 8, 40, 64), generator=g).half().to(cuda)
+    k1 = torch.randn((1, 8, 40, 128), generator=g).half().to(cuda)
+    v1 = torch.randn((1, 8, 40, 128), generator=g).half().to(cuda)
+    for kk, vv in ((k, v64), (k1, v1)):
+        want = F.scaled_dot_product_attention(q.float(), kk.float(), vv.float())
+        with tsa.sdpa_override():
+            got = F.scaled_dot_product_attention(q, kk, vv)
+        assert got.shape == want.shape
+        assert_close(got, want.cpu())
+
+
 # ----------------------------------------------------------------- opcheck --
 
 def _opcheck_cases(cuda):

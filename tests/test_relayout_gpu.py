@@ -304,14 +304,6 @@ def test_empty_and_errors(cuda):
         tsa.relayout.h2d_buffer(torch.zeros(64, 64, dtype=torch.float16), stl)
 
 
-# Whole-tile nests for the stepped kernels: 1 to 4 tile loops, lengths that
-# are powers of two and lengths that are not.  (sizes, padded length of dim
-# 1 of the host buffer the tensor is a view of, or None for a contiguous
-# tensor: the padding keeps the two leading loops from merging.)
-#   [64, 2048]        to sticks: A tiles 2               from: B tiles 2 (32 x 32)
-#   [96, 4096]        to: B tiles 2, A tiles 3            from: B tiles 6 (64 x 16)
-#   [3, 64, 4096]     to: B 2, A 2, outer 3               from: B 4, outer 3
-#   [3, 5, 64, 4096]  to: B 2, A 2, outer 5, outer 3      from: B 4, outer 5, 3
 # Row-major <-> default sticks through the stepped stick-tile kernel.  The
 # stick loop (host dim 0 in the default layout) and the last dim's sticks
 # form the tiles; the remaining loops step whole tiles.  Loops that are

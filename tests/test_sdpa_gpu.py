@@ -663,8 +663,9 @@ def test_key_stride_near_the_descriptor_limit(cuda, Sq):
 
 # Decode calls whose (sequence, KV head, chunk) grid fills at least half the
 # device stream dense K / V through the split-KV decode kernels: one chunk
-# per sequence, or several and the merge pass; a ragged last 64-token run;
-# g = 1 and 16; K / V rows padded past D; D = 128 and 64.
+# per sequence, or several and the merge pass; a ragged last 64-token run
+# (read as the 64-token window ending with the last key); contexts shorter
+# than one run; g = 1 and 16; K / V rows padded past D; D = 128 and 64.
 DENSE_DECODE_CASES = [
     (32, 32, 8, 4096, 0, 128),  # Llama-3-8B decode: one chunk per (sequence, KV head)
     (4, 32, 8, 32768, 0, 128),  # long context: 8 chunks and the merge pass
@@ -677,6 +678,9 @@ DENSE_DECODE_CASES = [
     (32, 32, 8, 4096, 0, 64),  # D = 64
     (8, 32, 8, 16384, 0, 64),  # D = 64, chunks and the merge pass
     (32, 16, 16, 2047, 8, 64),  # D = 64, g = 1, K / V rows 72 features apart, a ragged last run
+    (64, 32, 8, 40, 0, 128),  # a context shorter than one run: per-lane offsets, tokens past it out of range
+    (32, 16, 16, 33, 8, 64),  # D = 64, shorter than one run, K / V rows 72 features apart
+    (64, 32, 8, 65, 0, 128),  # the last run a window of 64 tokens with one of its own
 ]
 
 
@@ -704,7 +708,8 @@ def test_dense_decode_through_split_kernels(cuda, B, Hq, Hkv, Skv, pad, D):
     assert err <= 1e-4, err
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad,D", [DENSE_DECODE_CASES[i] for i in (1, 2, 4, 9, 10)], ids=str)
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,pad,D", [DENSE_DECODE_CASES[i] for i in (1, 2, 4, 9, 10, 11, 12, 13)],
+                         ids=str)
 def test_dense_decode_counts_every_key_once(cuda, B, Hq, Hkv, Skv, pad, D):
     """q = 0: every score is 0, so LSE = ln(Skv) up to the fp32 rounding of
     the log (a lost or doubled key moves it by at least 1/Skv) and out is the
@@ -791,8 +796,11 @@ def test_random_calls_across_routes(cuda, B, Hq, Hkv, Sq, Skv, D, causal):
 @pytest.mark.parametrize("D", [64, 128])
 def test_dense_decode_ignores_rows_past_the_keys(cuda, D):
     """K / V views of the first Skv rows of a larger cache whose later rows
-    hold NaN: a ragged last run must read nothing past row Skv - 1 (the
-    split-KV kernels' buffer range ends with the last key)."""
+    hold NaN: the rows past the keys weigh nothing (finite LSE, out equal to
+    the oracle's).  That no load touches them -- the last, ragged run is read
+    as the 64-token window ending with the last key -- is checked for every
+    lane and load on the CPU (test_decode_addresses.py); NaN there would
+    show only if such a row were given weight."""
     B, Hq, Hkv, Skv, Smax = 32, 32, 8, 2000, 2048
     q = randn((B, Hq, 1, D), SEED + 160)
     kf, vf = randn((B, Hkv, Smax, D), SEED + 161), randn((B, Hkv, Smax, D), SEED + 162)

@@ -79,6 +79,8 @@ SIGNATURES = {
     "spyre_paged_decode_attn_noalloc_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                                     c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                                     c_int64, c_int, c_int, c_float, c_void_p]),
+    "spyre_dense_decode_load_extent": (c_int, [c_int, c_int, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
+                                               POINTER(c_int64)]),
     "spyre_sdpa_fwd_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "spyre_sdpa_fwd_call_workspace_bytes": (c_size_t, [c_void_p, c_int, POINTER(c_int64), c_int, c_int, c_int,
                                                        c_int, c_int, c_int]),

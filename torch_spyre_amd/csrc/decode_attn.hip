@@ -45,6 +45,7 @@
 #include <atomic>
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 
 #include "decode_dense.h"
 #include "spyre_common.h"
@@ -52,6 +53,7 @@
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPage = 64;
@@ -137,8 +139,35 @@ __device__ __forceinline__ f16x8 ror8(f16x8 x) {
   return __builtin_bit_cast(f16x8, v);
 }
 
-__device__ __forceinline__ int chunk_x(int lane) { return (lane & 8) ? 4 + (lane >> 4) : (lane >> 4); }
-__device__ __forceinline__ int chunk_y(int lane) { return (lane & 8) ? (lane >> 4) : 4 + (lane >> 4); }
+__host__ __device__ __forceinline__ int chunk_x(int lane) { return (lane & 8) ? 4 + (lane >> 4) : (lane >> 4); }
+__host__ __device__ __forceinline__ int chunk_y(int lane) { return (lane & 8) ? (lane >> 4) : 4 + (lane >> 4); }
+
+// ---- Dense route addresses (K / V as [tokens, D] rows) -------------------
+//
+// One 64-token run of a dense K / V head is read by these loads (lane l):
+//   K load (jh, t, y): token dense_k_tok(l, y) + dense_k_dtok(jh), bytes
+//     dense_k_col(l, y) + 128 t .. + 15 of the token's row (t < D / 64);
+//   V load (j, i):     token dense_v_tok(l) + 32 j + i, bytes
+//     dense_v_col<D>(l) .. + kDenseVBytes<D> - 1.
+// Every byte lies inside the first 2 D bytes of its token's row.  The
+// kernel and the host-side check (spyre_dense_decode_load_extent) use
+// these same functions.
+__host__ __device__ __forceinline__ int dense_k_tok(int lane, bool y) {
+  const int r = lane & 7;
+  return 8 * (r >> 2) + (r & 3) + (y ? 16 : 0);  // QK block 0's token of MFMA row r (X) or 8 + r (Y)
+}
+__host__ __device__ __forceinline__ int dense_k_dtok(int jh) { return 32 * (jh >> 1) + 4 * (jh & 1); }
+__host__ __device__ __forceinline__ int dense_k_col(int lane, bool y) { return 16 * (y ? chunk_y(lane) : chunk_x(lane)); }
+__host__ __device__ __forceinline__ int dense_v_tok(int lane) { return 8 * (lane >> 4); }
+// D = 128: features 8f .. 8f + 7, f = l & 15 (16 bytes).  D = 64: features
+// 8f + 4h .. + 3, f = l & 7, h = (l >> 3) & 1 (8 bytes): lanes 8-15 of a row
+// start half a block on, so that MFMA row i's feature is 8 (i & 7) + 4 (i >> 3) + db.
+template <int D>
+__host__ __device__ __forceinline__ int dense_v_col(int lane) {
+  return D == 128 ? 16 * (lane & 15) : 16 * (lane & 7) + 8 * ((lane >> 3) & 1);
+}
+template <int D>
+constexpr int kDenseVBytes = D == 128 ? 16 : 8;
 
 // Builds the operand pair from the raw X / Y loads (in place).
 __device__ __forceinline__ void shuffle_pair(f16x8& x, f16x8& y, bool bit3) {
@@ -164,6 +193,19 @@ __device__ __forceinline__ f16x8 bload(Rsrc r, int voff, int soff) {
   return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT));
 }
 
+// The dense V operand registers of one token: 8 features (D = 128) or 4
+// (D = 64).
+template <int D>
+using DenseV = typename std::conditional<D == 128, f16x8, f16x4>::type;
+
+template <int D>
+__device__ __forceinline__ DenseV<D> bload_v(Rsrc r, int voff, int soff) {
+  if constexpr (D == 128)
+    return bload(r, voff, soff);
+  else
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kLoadNT));
+}
+
 // Per-lane byte offsets of the raw loads (see the X / Y scheme above).
 struct LoadOffsets {
   int kx, ky, vx, vy;
@@ -171,23 +213,23 @@ struct LoadOffsets {
     const int r = lane & 7, cx = chunk_x(lane), cy = chunk_y(lane);
     // QK block jh = (j, h): MFMA row i <-> token 32j + 8(i/4) + 4h + i%4;
     // this is block 0's token of row r.
-    const int tx = 8 * (r >> 2) + (r & 3);
+    const int tx = dense_k_tok(lane, false);
     kx = (tx * 64 + cx * 8) * 2;
     ky = ((tx + 16) * 64 + cy * 8) * 2;     // row 8 + r is token tx + 16
     vx = (r * kPage + cx * 8) * 2;
     vy = ((8 + r) * kPage + cy * 8) * 2;
   }
-  // Dense K / V (head_dim d), tokens k_row / v_row bytes apart: the K
-  // loads as above; vx is the dense V load's offset (load_v_dense), vy
-  // unused.
-  __device__ __forceinline__ LoadOffsets(int lane, int k_row, int v_row, int d) {
-    const int r = lane & 7, cx = chunk_x(lane), cy = chunk_y(lane);
-    const int tx = 8 * (r >> 2) + (r & 3);
-    kx = tx * k_row + cx * 16;
-    ky = (tx + 16) * k_row + cy * 16;
-    const int fo = d == 128 ? 16 * (lane & 15) : 16 * (lane & 7) + 8 * ((lane >> 3) & 1);
-    vx = 8 * (lane >> 4) * v_row + fo;
-    vy = 0;
+  // Dense K / V (head_dim D), tokens k_row / v_row bytes apart: the K
+  // loads as above (dense_k_*); vx is the dense V load's offset
+  // (load_v_dense), vy unused.
+  template <int D>
+  __device__ __forceinline__ static LoadOffsets dense(int lane, int k_row, int v_row) {
+    LoadOffsets lo(lane);
+    lo.kx = dense_k_tok(lane, false) * k_row + dense_k_col(lane, false);
+    lo.ky = dense_k_tok(lane, true) * k_row + dense_k_col(lane, true);
+    lo.vx = dense_v_tok(lane) * v_row + dense_v_col<D>(lane);
+    lo.vy = 0;
+    return lo;
   }
 };
 
@@ -207,44 +249,54 @@ __device__ __forceinline__ void load_k(f16x8 (&ka)[4][D / 32], Rsrc kr, const Lo
 }
 
 // Dense K: the same X / Y stick loads, tokens k_row bytes apart (the
-// token's two 128-byte sticks side by side instead of 8 KiB apart).
-template <int D>
-__device__ __forceinline__ void load_k_dense(f16x8 (&ka)[4][D / 32], Rsrc kr, int kx, int ky, int k_row) {
+// token's two 128-byte sticks side by side instead of 8 KiB apart).  A
+// 64-token window (WHOLE) keeps the token offset in the scalar operand:
+// every load lies inside the window's rows.  A context shorter than 64
+// tokens is read as one short run (WHOLE false) with the whole offset in
+// the per-lane operand, which the buffer's range check covers (the range
+// ends with the last token's 2 D bytes): no byte past the context is read,
+// and the lanes of tokens past it load zeros (bytes inside the view when
+// the token stride is below 2 D bytes).
+template <int D, bool WHOLE>
+__device__ __forceinline__ void load_k_dense(f16x8 (&ka)[4][D / 32], Rsrc kr, const LoadOffsets& lo, int k_row) {
 #pragma unroll
-  for (int jh = 0; jh < 4; ++jh) {
+  for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
     for (int t = 0; t < D / 64; ++t) {
-      const int so = (32 * (jh >> 1) + 4 * (jh & 1)) * k_row + t * 128;
-      ka[jh][2 * t] = bload(kr, kx, so);
-      ka[jh][2 * t + 1] = bload(kr, ky, so);
+      const int so = dense_k_dtok(jh) * k_row + t * 128;
+      ka[jh][2 * t] = WHOLE ? bload(kr, lo.kx, so) : bload(kr, lo.kx + so, 0);
+      ka[jh][2 * t + 1] = WHOLE ? bload(kr, lo.ky, so) : bload(kr, lo.ky + so, 0);
     }
-  }
 }
 
 // Dense V ([tokens, D], tokens v_row bytes apart): lane l (token group tg =
-// l >> 4) loads 8 features of tokens 32j + 8tg + i into va[i][j], each
-// instruction four whole token rows.  D = 128: features 8f .. 8f + 7, f =
-// l & 15.  D = 64: features 8f + 4h .. + 7, f = l & 7, h = (l >> 3) & 1 (the
-// lanes of h = 1 start half a block on, and their last four features, past
-// the block, are never used).  transposed_col turns a j's eight registers
-// into the PV operands: MFMA db's row i is feature 8i + db (D = 128), or
-// 8 (i & 7) + 4 (i >> 3) + db (D = 64, db < 4).
-__device__ __forceinline__ void load_v_dense(f16x8 (&va)[8][2], Rsrc vr, int vo, int v_row) {
+// l >> 4) loads its features (dense_v_col) of tokens 32j + 8tg + i into
+// va[i][j], each instruction four whole token rows.  transposed_col turns a
+// j's eight registers into the PV operands: MFMA db's row i is feature
+// 8i + db (D = 128), or 8 (i & 7) + 4 (i >> 3) + db (D = 64, db < 4).
+// Windows and short runs as load_k_dense.
+template <int D, bool WHOLE>
+__device__ __forceinline__ void load_v_dense(DenseV<D> (&va)[8][2], Rsrc vr, const LoadOffsets& lo, int v_row) {
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) va[i][j] = bload(vr, vo, (32 * j + i) * v_row);
+    for (int i = 0; i < 8; ++i) {
+      const int so = (32 * j + i) * v_row;
+      va[i][j] = WHOLE ? bload_v<D>(vr, lo.vx, so) : bload_v<D>(vr, lo.vx + so, 0);
+    }
 }
 
 // Column a of the 8 x 8 block of 16-bit elements va[0..7][j]: element i is
 // va[i][j][a] (the a-th loaded feature of token 32j + 8tg + i).
-__device__ __forceinline__ f16x8 transposed_col(const f16x8 (&va)[8][2], int j, int a) {
+template <typename VT>
+__device__ __forceinline__ f16x8 transposed_col(const VT (&va)[8][2], int j, int a) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32w __attribute__((ext_vector_type(sizeof(VT) / 4)));
   u32x4 x;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const uint32_t lo = __builtin_bit_cast(u32x4, va[2 * p][j])[a / 2];
-    const uint32_t hi = __builtin_bit_cast(u32x4, va[2 * p + 1][j])[a / 2];
+    const uint32_t lo = __builtin_bit_cast(u32w, va[2 * p][j])[a / 2];
+    const uint32_t hi = __builtin_bit_cast(u32w, va[2 * p + 1][j])[a / 2];
     x[p] = (a & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
   }
   return __builtin_bit_cast(f16x8, x);
@@ -309,15 +361,41 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 
   // Page it's K/V resources (page id broadcast from lane it % 64).
   const int head_bytes = static_cast<int>(head_elems * 2);
-  // Dense: tokens 64 (p0 + it) .. + 63 of the sequence's K / V head, the
-  // range ending with the last token (the host keeps a 64-token run of
-  // either within 2^30 bytes, so no per-lane offset wraps).
+  // Dense: run it is tokens 64 (p0 + it) .. + 63 of the sequence's K / V
+  // head.  A short last run (ctx % 64 != 0, ctx >= 64) is read as the
+  // 64-token window ending with the last token, whose first tokens (the
+  // previous run's, already streamed) are masked out, so that every load of
+  // the steady state lies inside the view.  Only a context below 64 tokens
+  // is a short run: one run, loaded before the loop with the whole offset
+  // per lane (load_k_dense).  A resource's range ends with the last row's
+  // 2 D bytes (the host keeps 64 rows of either within 2^30 bytes, so no
+  // offset wraps).
   const int k_row = DENSE ? static_cast<int>(a.k_ss * 2) : 0, v_row = DENSE ? static_cast<int>(a.v_ss * 2) : 0;
+  // Run it's window: it starts lo_tok tokens before the run (0 but for a
+  // short last run of dense K / V: the wave's run shift_it, shifted by
+  // shift tokens), and its tokens [lo_tok, hi_tok) are the run's own.
+  int shift_it = -1, shift = 0;
+  if (DENSE && ctx >= kPage && ctx % kPage != 0 && p0 + n_it == pages_of(ctx)) {
+    shift_it = n_it - 1;
+    shift = kPage - ctx % kPage;
+  }
+  auto window = [&](int it, int& lo_tok, int& hi_tok) {
+    lo_tok = it == shift_it ? shift : 0;
+    hi_tok = min(kPage, ctx - (p0 + it) * kPage + lo_tok);
+  };
+  // Dense: the wave's first run; run it is run_bytes further on.
+  const char* k0 = DENSE ? reinterpret_cast<const char*>(a.k + b * a.k_sb + kvh * a.k_sh) +
+                               static_cast<int64_t>(p0) * kPage * k_row : nullptr;
+  const char* v0 = DENSE ? reinterpret_cast<const char*>(a.v + b * a.v_sb + kvh * a.v_sh) +
+                               static_cast<int64_t>(p0) * kPage * v_row : nullptr;
   auto locate = [&](int it, Rsrc& kr, Rsrc& vr) {
     if constexpr (DENSE) {
-      const int t0 = (p0 + it) * kPage, rows = min(kPage, ctx - t0);
-      kr = page_rsrc(a.k + b * a.k_sb + kvh * a.k_sh + t0 * a.k_ss, (rows - 1) * k_row + 2 * D);
-      vr = page_rsrc(a.v + b * a.v_sb + kvh * a.v_sh + t0 * a.v_ss, (rows - 1) * v_row + 2 * D);
+      int lo_tok, hi_tok;
+      window(it, lo_tok, hi_tok);
+      const char* kp = k0 + (static_cast<int64_t>(it) * kPage - lo_tok) * k_row;
+      const char* vp = v0 + (static_cast<int64_t>(it) * kPage - lo_tok) * v_row;
+      kr = page_rsrc(reinterpret_cast<const _Float16*>(kp), (hi_tok - 1) * k_row + 2 * D);
+      vr = page_rsrc(reinterpret_cast<const _Float16*>(vp), (hi_tok - 1) * v_row + 2 * D);
     } else {
       int64_t phys = __builtin_amdgcn_readlane(ids, it & 63);
       const bool bad = phys < 0 || phys >= a.num_pages;
@@ -327,23 +405,35 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
       vr = page_rsrc(a.v + phys * page_elems + kvh * head_elems, head_bytes);
     }
   };
-  const LoadOffsets lo = DENSE ? LoadOffsets(lane, k_row, v_row, D) : LoadOffsets(lane);
+  const LoadOffsets lo = DENSE ? LoadOffsets::dense<D>(lane, k_row, v_row) : LoadOffsets(lane);
+  // Loads of a whole run (a page, or a 64-token window of dense K / V).
   auto issue_k = [&](f16x8 (&ka)[4][DS], Rsrc kr) {
-    if constexpr (DENSE) load_k_dense<D>(ka, kr, lo.kx, lo.ky, k_row); else load_k<D>(ka, kr, lo);
+    if constexpr (DENSE) load_k_dense<D, true>(ka, kr, lo, k_row); else load_k<D>(ka, kr, lo);
   };
-  constexpr int VR = DENSE ? 8 : DB;  // V registers per token half
-  auto issue_v = [&](f16x8 (&va)[VR][2], Rsrc vr) {
-    if constexpr (DENSE) load_v_dense(va, vr, lo.vx, v_row); else load_v<D>(va, vr, lo);
+  // V registers: dense, 8 tokens x 2 halves of the run (DenseV<D> each);
+  // paged, DB feature blocks x 2 token halves.
+  using VT = typename std::conditional<DENSE, DenseV<D>, f16x8>::type;
+  constexpr int VR = DENSE ? 8 : DB;
+  auto issue_v = [&](VT (&va)[VR][2], Rsrc vr) {
+    if constexpr (DENSE) load_v_dense<D, true>(va, vr, lo, v_row); else load_v<D>(va, vr, lo);
   };
   Rsrc kr, vr;
   locate(0, kr, vr);
   f16x8 ka[4][DS];
-  f16x8 va[VR][2];
-  issue_k(ka, kr);
-  issue_v(va, vr);
+  VT va[VR][2];
+  if (DENSE && ctx < kPage) {
+    if constexpr (DENSE) {  // the one short run
+      load_k_dense<D, false>(ka, kr, lo, k_row);
+      load_v_dense<D, false>(va, vr, lo, v_row);
+    }
+  } else {
+    issue_k(ka, kr);
+    issue_v(va, vr);
+  }
 
   for (int it = 0; it < n_it; ++it) {
-    const int valid = min(kPage, ctx - (p0 + it) * kPage);
+    int lo_tok, valid;  // this run's own window tokens: [lo_tok, valid)
+    window(it, lo_tok, valid);
     const bool bit3 = (lane & 8) != 0;
 #pragma unroll
     for (int jh = 0; jh < 4; ++jh)
@@ -370,16 +460,25 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
     }
 
     // This lane holds head col's scores for tokens 32j + 8grp + 4h + v.
+    // Tokens outside [lo_tok, valid) score -inf; a whole run (every run but
+    // a sequence's last) skips the comparisons by a wave-uniform branch.
     float mx = -INFINITY;
+    auto scale_scores = [&](auto edge) {
 #pragma unroll
-    for (int jh = 0; jh < 4; ++jh)
+      for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int t = 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
-        const float x = t < valid ? sc[jh][v] * a.scale_log2 : -INFINITY;
-        sc[jh][v] = x;
-        mx = fmaxf(mx, x);
-      }
+        for (int v = 0; v < 4; ++v) {
+          const int t = 32 * (jh >> 1) + 8 * grp + 4 * (jh & 1) + v;
+          float x = sc[jh][v] * a.scale_log2;
+          if constexpr (decltype(edge)::value) x = t >= lo_tok && t < valid ? x : -INFINITY;
+          sc[jh][v] = x;
+          mx = fmaxf(mx, x);
+        }
+    };
+    if (lo_tok > 0 || valid < kPage)
+      scale_scores(std::true_type{});
+    else
+      scale_scores(std::false_type{});
     mx = fmaxf(mx, wave_xor(mx, 16));
     mx = fmaxf(mx, wave_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
@@ -399,15 +498,10 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] *= alpha;
     if constexpr (DENSE) {
-      // va[i][j] holds token 32j + 8grp + i; past the context it may hold
-      // any bits (even NaN): zero it so that 0 * V stays 0.
-      if (valid < kPage) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            if (32 * j + 8 * grp + i >= valid) va[i][j] = f16x8{};
-      }
+      // va[i][j] holds window token 32j + 8grp + i.  Tokens below lo_tok
+      // are the view's own and weigh 0; past a short context the loads were
+      // out of range and gave zeros (token strides are 0 or at least 2 D
+      // bytes; with 0 every token is the one row), so 0 * V stays 0.
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -900,6 +994,10 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
     SPYRE_REQUIRE(k_strides[i] >= 0 && v_strides[i] >= 0, SPYRE_EUNSUPPORTED, "dense decode: negative stride");
   SPYRE_REQUIRE(k_strides[2] < (int64_t{1} << 23) && v_strides[2] < (int64_t{1} << 23), SPYRE_EUNSUPPORTED,
                 "dense decode: token stride 2^23 elements or more");
+  // Rows of whole tokens (a short context's loads of tokens past it are
+  // then wholly out of range, load_k_dense), or one row for every token.
+  SPYRE_REQUIRE((k_strides[2] == 0 || k_strides[2] >= D) && (v_strides[2] == 0 || v_strides[2] >= D),
+                SPYRE_EUNSUPPORTED, "dense decode: token stride between 0 and head_dim");
   SplitArgs sa{};
   sa.q = static_cast<const _Float16*>(q);
   sa.k = static_cast<const _Float16*>(k);
@@ -943,6 +1041,58 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
 }
 
 }  // namespace spyre_hip
+
+// ------------------------------------------- dense route address check --
+
+namespace {
+
+// Every load of the dense route's run of `rows` tokens (64: a window,
+// load_*_dense<D, true>; fewer: a short context, load_*_dense<D, false>):
+// f(is_k, voffset, soffset, width) with the per-lane and scalar byte
+// offsets the kernel passes.
+template <typename F>
+void for_each_dense_load(int D, int rows, int64_t k_row, int64_t v_row, F&& f) {
+  const bool whole = rows == kPage;
+  for (int lane = 0; lane < 64; ++lane) {
+    for (int jh = 0; jh < 4; ++jh)
+      for (int t = 0; t < D / 64; ++t)
+        for (int y = 0; y < 2; ++y) {
+          const int64_t base = dense_k_tok(lane, y) * k_row + dense_k_col(lane, y);  // LoadOffsets::dense
+          const int64_t so = dense_k_dtok(jh) * k_row + 128 * t;
+          f(true, whole ? base : base + so, whole ? so : 0, 16);
+        }
+    for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < 8; ++i) {
+        const int col = D == 128 ? dense_v_col<128>(lane) : dense_v_col<64>(lane);
+        const int w = D == 128 ? kDenseVBytes<128> : kDenseVBytes<64>;
+        const int64_t base = dense_v_tok(lane) * v_row + col, so = (32 * j + i) * v_row;
+        f(false, whole ? base : base + so, whole ? so : 0, w);
+      }
+  }
+}
+
+}  // namespace
+
+extern "C" int spyre_dense_decode_load_extent(int D, int rows, int64_t k_row, int64_t v_row, int64_t* k_end,
+                                              int64_t* v_end, int64_t* n_loads) {
+  spyre_hip::clear_error();
+  SPYRE_REQUIRE(D == 64 || D == 128, SPYRE_EINVAL, "head_dim %d not in {64, 128}", D);
+  SPYRE_REQUIRE(rows >= 1 && rows <= kPage, SPYRE_EINVAL, "rows %d not in [1, %d]", rows, kPage);
+  SPYRE_REQUIRE(k_row >= 0 && v_row >= 0 && k_end && v_end && n_loads, SPYRE_EINVAL, "bad arguments");
+  // The resources' ranges (stream_pages' locate).  A load is counted as
+  // touching memory unless its per-lane offset alone is out of range -- the
+  // range check is not assumed to cover the scalar offset -- and then as
+  // touching every byte up to voffset + soffset + width.
+  const int64_t k_range = (rows - 1) * k_row + 2 * D, v_range = (rows - 1) * v_row + 2 * D;
+  *k_end = *v_end = *n_loads = 0;
+  for_each_dense_load(D, rows, k_row, v_row, [&](bool is_k, int64_t voff, int64_t soff, int w) {
+    if (voff >= (is_k ? k_range : v_range)) return;  // out of range: zeros, no access
+    int64_t& e = is_k ? *k_end : *v_end;
+    e = std::max(e, voff + soff + w);
+    ++*n_loads;
+  });
+  return SPYRE_OK;
+}
 
 // ------------------------------------------ the entry that allocates nothing --
 

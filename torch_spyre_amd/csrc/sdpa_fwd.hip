@@ -1894,6 +1894,7 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
   if (lds_path) {
     const spyre_hip::DenseDecodePlan dp = dense_route(B, Hq, Hkv, Sq, Skv, D, is_causal != 0, mask_kind);
     if (dp.ok && k_strides[2] < (int64_t{1} << 23) && v_strides[2] < (int64_t{1} << 23) &&
+        (k_strides[2] == 0 || k_strides[2] >= D) && (v_strides[2] == 0 || v_strides[2] >= D) &&
         (dp.ws_bytes == 0 || (workspace && aligned16(workspace) && workspace_bytes >= dp.ws_bytes)))
       return spyre_hip::dense_decode_launch(dp, q, q_strides, k, k_strides, v, v_strides, out, lse, workspace, B,
                                             Hq, Hkv, Skv, D, scale, stream);

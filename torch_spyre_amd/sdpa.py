@@ -229,6 +229,12 @@ def _servable(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
         return False
     if query.shape[-1] not in (64, 128) or key.shape[-1] != query.shape[-1] or dropout_p > 0.0:
         return False
+    # value must match key exactly and the batch must match query: torch
+    # serves other shapes (another value head dim, broadcast batch dims)
+    if value.shape != key.shape or query.shape[0] != key.shape[0]:
+        return False
+    if not (query.device == key.device == value.device):
+        return False
     if key.shape[1] == 0 or query.shape[1] % key.shape[1] or (query.shape[1] != key.shape[1] and not enable_gqa):
         return False
     if attn_mask is not None and (is_causal or not isinstance(attn_mask, torch.Tensor)
