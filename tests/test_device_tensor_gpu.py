@@ -232,3 +232,149 @@ def test_strided_host_source_round_trip(cuda):
     assert np.array_equal(_raw(d.cpu()), bits.T)
     r = tsa.restickify(d, tsa.SpyreTensorLayout([256, 192], [1, 256], torch.float16, [1, 0]))
     assert np.array_equal(_raw(r.cpu()), bits.T)
+
+
+# ------------------------------------------------- KV-cache writes (boxes) --
+
+def _cache(cuda, seed):
+    """A [1, 8, 2048, 128] fp16 KV cache in its default stick layout
+    (tests/inductor/test_inductor_ops.py:5688-5739), and its host bits."""
+    import torch_spyre_amd as tsa
+
+    bits, x = _bits((1, 8, 2048, 128), seed, cuda)
+    return bits, tsa.to_device_layout(x, tsa.SpyreTensorLayout([1, 8, 2048, 128], torch.float16))
+
+
+def _device_want(host_bits):
+    size = list(host_bits.shape)
+    return OL.h2d(host_bits.reshape(-1), size, OL.contiguous_strides(size), 0, OL.stl_default(size))
+
+
+def test_token_write_by_slice_select_and_index_copy(cuda):
+    """Decode writes into a stick-layout cache: a token by slice copy_, one by
+    select copy_, one by index_copy_ (the reference's decode pattern,
+    tests/inductor/test_inductor_ops.py:5715-5739) and a 14-token prefill
+    by index_copy_ (:5688-5713): the device bytes equal the oracle's layout of
+    the cache with the tokens written, and every write moved only its own
+    elements."""
+    from torch_spyre_amd import device_tensor as DT
+
+    bits, cache = _cache(cuda, SEED + 200)
+    want = bits.copy()
+    t1b, t1 = _bits((1, 8, 1, 128), SEED + 201, cuda)
+    cache[:, :, 14:15, :].copy_(t1)
+    want[:, :, 14:15, :] = t1b
+    t2b, t2 = _bits((1, 8, 128), SEED + 202, cuda)
+    cache[:, :, 15, :].copy_(t2)
+    want[:, :, 15, :] = t2b
+    t3b, t3 = _bits((1, 8, 1, 128), SEED + 203, cuda)
+    res = cache.index_copy_(2, torch.tensor([16], dtype=torch.int64), t3)
+    assert res is cache
+    want[:, :, 16:17, :] = t3b
+    pb, p = _bits((1, 8, 14, 128), SEED + 204, cuda)
+    cache.index_copy_(2, torch.arange(100, 114, dtype=torch.int64, device=cuda), p)
+    want[:, :, 100:114, :] = pb
+    assert np.array_equal(_raw(cache).reshape(-1), _device_want(want))
+    # the writes' loop nests move exactly the token's elements
+    v = cache[:, :, 14:15, :]
+    infos = DT._box_infos(v, t1, host2device=True)
+    assert sum(int(np.prod(i.size[:i.rank])) for i in infos) == t1.numel()
+    # reading a token back moves only its elements too, and equals the oracle
+    assert np.array_equal(_raw(cache[:, :, 100:114, :].cpu()), pb)
+
+
+def test_index_copy_out_of_place_and_errors(cuda):
+    """index_copy (out of place) leaves self unchanged; indices out of range
+    and shape mismatches raise."""
+    bits, cache = _cache(cuda, SEED + 210)
+    tb, t = _bits((1, 8, 2, 128), SEED + 211, cuda)
+    out = torch.index_copy(cache, 2, torch.tensor([5, 2047]), t)
+    want = bits.copy()
+    want[:, :, 5], want[:, :, 2047] = tb[:, :, 0], tb[:, :, 1]
+    assert np.array_equal(_raw(out).reshape(-1), _device_want(want))
+    assert np.array_equal(_raw(cache).reshape(-1), _device_want(bits))
+    with pytest.raises(IndexError):
+        cache.index_copy_(2, torch.tensor([2048]), t[:, :, :1])
+    with pytest.raises(IndexError):
+        cache.index_copy_(2, torch.tensor([1, 2, 3]), t)
+
+
+def test_box_writes_across_sticks(cuda):
+    """Writes into boxes that start and end inside sticks, of the default and
+    the transposed ([1, 0]) layouts, and through a transposed view: bit-exact
+    against the oracle."""
+    import torch_spyre_amd as tsa
+
+    size = [130, 200]
+    for k, order in enumerate(([0, 1], [1, 0])):
+        bits, x = _bits(tuple(size), SEED + 220 + k, cuda)
+        stl = tsa.SpyreTensorLayout(size, [200, 1], torch.float16, order)
+        d = tsa.to_device_layout(x, stl)
+        want = bits.copy()
+        ab, a = _bits((97, 145), SEED + 230 + k, cuda)
+        d[3:100, 5:150].copy_(a)
+        want[3:100, 5:150] = ab
+        bb, b = _bits((100, 40), SEED + 240 + k, cuda)
+        d.t()[20:120, 10:50].copy_(b)
+        want.T[20:120, 10:50] = bb
+        ol = OL.Layout(list(stl.device_size), list(stl.stride_map), "float16")
+        assert np.array_equal(_raw(d).reshape(-1), OL.h2d(want.reshape(-1), size, [200, 1], 0, ol))
+        assert np.array_equal(_raw(d[7:90, 33:180].cpu()), want[7:90, 33:180])
+
+
+# --------------------------------------------------- views carrying layouts --
+
+def test_views_with_layout(cuda):
+    """as_strided_with_layout / reinterpret_tensor[_with_layout]
+    (torch_spyre/csrc/spyre_views.cpp:123-181): with the tensor's own layout
+    a view keeps the DMA geometry (reads equal the host view); with another
+    layout the allocation's bytes are read through the new layout and the
+    view's own geometry (bit-exact against the oracle's D2H of the raw
+    bytes)."""
+    import torch_spyre_amd as tsa
+
+    bits, x = _bits((256, 192), SEED + 250, cuda)
+    d = tsa.to_device_layout(x, tsa.SpyreTensorLayout([256, 192], torch.float16))
+    v = tsa.as_strided_with_layout(d, [64, 192], [192, 1], 192 * 10, d.device_tensor_layout())
+    assert np.array_equal(_raw(v.cpu()), bits[10:74])
+    r = tsa.reinterpret_tensor(d, [32, 192], [192, 1], 192 * 100)
+    assert np.array_equal(_raw(r.cpu()), bits[100:132])
+    raw = _raw(d).reshape(-1)
+    # the 96 KiB allocation as [128, 384] in its default layout
+    stl2 = tsa.SpyreTensorLayout([128, 384], torch.float16)
+    w = tsa.reinterpret_tensor_with_layout(d, [128, 384], [384, 1], 0, stl2)
+    assert w.device_tensor_layout() == stl2 and w.data_ptr() == d.data_ptr()
+    assert np.array_equal(_raw(w.cpu()), OL.d2h(raw, [128, 384], OL.stl_default([128, 384])))
+    a = tsa.as_strided_with_layout(d, [128, 384], [384, 1], 0, stl2)
+    assert np.array_equal(_raw(a.cpu()), OL.d2h(raw, [128, 384], OL.stl_default([128, 384])))
+    with pytest.raises(ValueError):  # more than the allocation holds
+        tsa.reinterpret_tensor_with_layout(d, [512, 192], [192, 1], 0, tsa.SpyreTensorLayout([512, 192],
+                                                                                            torch.float16))
+
+
+def test_tensor_to_device_layout_and_empty(cuda):
+    """The reference's method forms (torch_spyre/_monkey_patch.py:63-196):
+    x.to(device_layout=) from CPU and GPU host order and between layouts,
+    torch.empty(..., device_layout=), Tensor.device_tensor_layout()."""
+    import torch_spyre_amd as tsa
+
+    bits, x = _bits((256, 192), SEED + 260, cuda)
+    stl = tsa.SpyreTensorLayout([256, 192], torch.float16)
+    tr = tsa.SpyreTensorLayout([256, 192], [192, 1], torch.float16, [1, 0])
+    d = x.cpu().to(device_layout=stl)
+    assert isinstance(d, tsa.SpyreTensor) and d.device_tensor_layout() == stl
+    assert np.array_equal(_raw(d).reshape(-1), OR.to_sticks(bits).reshape(-1))
+    d2 = x.to(device_layout=stl)
+    assert np.array_equal(_raw(d2).reshape(-1), OR.to_sticks(bits).reshape(-1))
+    assert d2.to(device_layout=stl) is d2 and d2.to(device_layout=stl, copy=True) is not d2
+    t = d2.to(device_layout=tr)
+    assert t.device_tensor_layout() == tr and np.array_equal(_raw(t).reshape(-1), OR.transpose_restick(bits).reshape(-1))
+    assert np.array_equal(_raw(t.cpu()), bits)
+    assert x.device_tensor_layout() is None
+    e = torch.empty(256, 192, dtype=torch.float16, device_layout=stl)
+    assert isinstance(e, tsa.SpyreTensor) and e.device_tensor_layout() == stl and list(e.shape) == [256, 192]
+    e.copy_(x)
+    assert np.array_equal(_raw(e).reshape(-1), OR.to_sticks(bits).reshape(-1))
+    assert torch.empty(3, 4).device_tensor_layout() is None  # torch's own otherwise
+    f = x.to(torch.float32, device_layout=tsa.SpyreTensorLayout([256, 192], torch.float32))
+    assert f.dtype == torch.float32 and torch.equal(f.cpu(), x.float().cpu())

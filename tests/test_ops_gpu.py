@@ -90,6 +90,41 @@ def test_overwrite_ops_vs_oracle(cuda):
     assert np.array_equal(_raw(out), want)
 
 
+def test_overwrite_f_in_compiled_loop(cuda):
+    """tests/inductor/test_overwrite.py:208-241: a torch.compile'd loop of
+    spyre::overwrite_f, one token per slot.  The result equals the oracle's
+    overwrites bit for bit; inductor's reinplace pass (the registration of
+    torch_spyre/_inductor/customops.py:333-335) turns every overwrite_f after
+    the first (which reads the graph input, not mutated) into an in-place
+    overwrite of that one copy, so the generated code copies the cache once
+    instead of once per token."""
+    from torch._inductor.utils import run_and_get_code
+
+    slots = [3, 11, 7, 19]
+
+    def scatter(cache, tokens):
+        for i in range(len(slots)):
+            cache = torch.ops.spyre.overwrite_f(tokens[i:i + 1], cache, [0], [slots[i]])
+        return cache
+
+    torch._dynamo.reset()
+    cb, cache = _bits((32, 4, 64), SEED + 20, cuda)
+    tb, tokens = _bits((4, 4, 64), SEED + 21, cuda)
+    result, codes = run_and_get_code(torch.compile(scatter), cache, tokens)
+    want = cb.copy()
+    for i, s in enumerate(slots):
+        OK.overwrite(tb[i:i + 1], want, [0], [s])
+    assert np.array_equal(_raw(result), want)
+    assert np.array_equal(_raw(cache), cb)  # the input is unchanged
+    code = "\n".join(codes)
+    # the first write reads the graph input, which is not mutated: one
+    # overwrite_f (its one copy of the cache); every later one in place
+    functional = code.count("torch.ops.spyre.overwrite_f.default(")
+    assert functional <= 1, code
+    assert code.count("torch.ops.spyre.overwrite.default(") == len(slots) - functional, code
+    assert code.count("clone") + code.count(".copy_(") == 0, code
+
+
 def test_kv_append_and_paged_decode_ops_vs_oracle(cuda):
     """spyre::kv_append then spyre::paged_decode_attention: the caches equal
     the oracle's append on logical pages (bit-exact), the attention its CPU

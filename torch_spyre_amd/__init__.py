@@ -37,6 +37,9 @@ from .device_tensor import (  # noqa: E402
     set_restickify_target,
     spyre_empty_with_layout,
     to_device_layout,
+    as_strided_with_layout,
+    reinterpret_tensor,
+    reinterpret_tensor_with_layout,
 )
 from .attention import (  # noqa: E402
     PagedDecode,
@@ -59,12 +62,16 @@ from .sdpa import (  # noqa: E402
     sdpa_overrideable,
 )
 from . import ops  # noqa: E402,F401  (registers the spyre:: ops)
+from . import _torch_patch  # noqa: E402
+
+_torch_patch.apply()  # Tensor.to(device_layout=), torch.empty(device_layout=), Tensor.device_tensor_layout()
 
 __all__ = [
     "DataFormats", "ElementArrangement", "SpyreTensorLayout", "dma_plan", "get_device_dtype",
     "restick_plan", "DmaCopy", "overwrite", "transpose_restick_layout",
     "SpyreTensor", "copy_tensor", "device_buffer", "device_tensor_layout", "from_device_layout", "restickify",
     "restickify_target_layout", "set_restickify_target", "spyre_empty_with_layout", "to_device_layout",
+    "as_strided_with_layout", "reinterpret_tensor", "reinterpret_tensor_with_layout",
     "PagedDecode", "PagedKVCache", "dense_to_pages", "k_page_layout", "kv_append", "paged_decode_attention",
     "paged_decode_merge", "paged_decode_split",
     "sdpa_decode", "v_page_layout", "workspace_bytes",

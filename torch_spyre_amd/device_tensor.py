@@ -16,7 +16,9 @@ dispatcher serves
 
 * view ops (geometry computed on a meta twin, buffer and layout shared);
 * ``.cpu()`` / ``.to("cpu")`` (D2H), ``copy_`` in every direction (H2D,
-  D2H, D2D between layouts), ``clone``;
+  D2H, D2D between layouts), ``clone``, ``index_copy_``; a view that is a
+  box of the allocation (slices, selects, permuted dims) moves only its own
+  elements;
 * ``spyre::restickify(x)`` (the reference's one-tensor schema,
   torch_spyre/_inductor/customops.py:338-342) and ``spyre::copy_from_d2d``
   (:240-257).
@@ -216,6 +218,51 @@ def device_buffer(t: SpyreTensor) -> torch.Tensor:
     return t._data
 
 
+def _relabel(x: SpyreTensor, size, stride, offset: int, layout: SpyreTensorLayout) -> SpyreTensor:
+    """x's allocation seen with (size, stride, offset) in ``layout``: the
+    DMA geometry stays x's when the layout does, else it becomes (size,
+    stride) (torch_spyre/csrc/spyre_views.cpp:137-143, :168-174)."""
+    if not isinstance(x, SpyreTensor):
+        raise TypeError("expected a SpyreTensor")
+    if not isinstance(layout, SpyreTensorLayout):
+        raise TypeError("device_layout must be a SpyreTensorLayout")
+    size, stride = [int(v) for v in size], [int(v) for v in stride]
+    if len(size) != len(stride):
+        raise ValueError("size and stride differ in length")
+    if layout == x._layout:
+        return SpyreTensor(x._data, layout, x._dma_size, x._dma_stride, size, stride, int(offset))
+    need = R.alloc_bytes(size, x.dtype, layout)
+    have = x._data.untyped_storage().nbytes()
+    if need > have:
+        raise ValueError(f"the allocation holds {have} bytes; {list(size)} in {layout} needs {need}")
+    return SpyreTensor(x._data, layout, size, stride, size, stride, int(offset))
+
+
+def as_strided_with_layout(x: SpyreTensor, size: Sequence[int], stride: Sequence[int],
+                           storage_offset: Optional[int], device_layout: SpyreTensorLayout) -> SpyreTensor:
+    """A view of x's allocation with (size, stride, storage_offset -- x's
+    when None) in ``device_layout`` (torch_spyre/csrc/spyre_views.cpp:123-146,
+    bound at torch_spyre/csrc/module.cpp:290)."""
+    off = x.storage_offset() if storage_offset is None else int(storage_offset)
+    return _relabel(x, size, stride, off, device_layout)
+
+
+def reinterpret_tensor(x: SpyreTensor, size: Sequence[int], stride: Sequence[int],
+                       offset_increment: int = 0) -> SpyreTensor:
+    """x's allocation as (size, stride) at x's offset + offset_increment, in
+    x's layout (torch_spyre/csrc/spyre_views.cpp:148-157)."""
+    return reinterpret_tensor_with_layout(x, size, stride, offset_increment, x._layout)
+
+
+def reinterpret_tensor_with_layout(x: SpyreTensor, size: Sequence[int], stride: Sequence[int],
+                                   offset_increment: int, stl: SpyreTensorLayout) -> SpyreTensor:
+    """x's allocation as (size, stride) at x's offset + offset_increment in
+    layout ``stl``: the reference's buffer reuse in generated code
+    (torch_spyre/csrc/spyre_views.cpp:159-181, emitted by
+    torch_spyre/_inductor/wrapper.py:149)."""
+    return _relabel(x, size, stride, x.storage_offset() + int(offset_increment), stl)
+
+
 # ----------------------------------------------------------------- copies --
 
 def _d2h_base(t: SpyreTensor) -> torch.Tensor:
@@ -227,8 +274,191 @@ def _d2h_base(t: SpyreTensor) -> torch.Tensor:
 def _d2h(t: SpyreTensor) -> torch.Tensor:
     if t.is_base():
         return _d2h_base(t)
+    # the view's strides when they are dense and non-overlapping, as clone()
+    # keeps them; else contiguous
+    out = torch.empty_like(t._meta(), device=t.device)
+    if t.numel() == 0:
+        return out
+    infos = _box_infos(t, out, host2device=False)
+    if infos is not None:  # a box: its own elements only
+        _run_infos(t._data, out, infos)
+        return out
     view = _d2h_base(t).as_strided(t.shape, t.stride(), t.storage_offset())
     return view.clone()  # keeps dense strides, else contiguous
+
+
+# ------------------------------------------------------- views as boxes --
+#
+# A view that selects a box of the allocation's host geometry -- slices,
+# selects, narrows and permutations of its dims, each view dim stepping one
+# host dim by 1 -- is moved by loop nests of its own, so its bytes are moved
+# and no others.  The layout must tile each host dim (of more than one
+# element) as the reference's tilings do: a unit device dim whose stride_map
+# is the host stride and, when that does not hold the whole dim, a tile dim
+# above it whose stride_map is the unit dim's run times the host stride (the
+# stick dim: runs of 64 elements).  Element (host coords c) then sits at the
+# row-major device position sum_j (c_j % run_j) RM[unit_j] + (c_j // run_j)
+# RM[tile_j].  A box that crosses run boundaries along a host dim is cut
+# there: the part before the first boundary, the whole runs (a tile loop and
+# a unit loop) and the part after the last one.  Other views and layouts
+# take the round trip through the whole geometry.
+
+def _dim_owners(layout: SpyreTensorLayout, dma_size, dma_stride):
+    """{host dim: (unit device dim, tile device dim or None, run)} for the
+    host dims of more than one element, or None when the layout does not
+    tile the geometry that way."""
+    ds, sm = list(layout.device_size), list(layout.stride_map)
+    owners, claimed = {}, set()
+    for j, (n, hs) in enumerate(zip(dma_size, dma_stride)):
+        if n <= 1:
+            continue
+        unit = [d for d in range(len(ds)) if sm[d] == hs and ds[d] > 1]
+        if len(unit) != 1:
+            return None
+        u = unit[0]
+        run = ds[u]
+        tile = None
+        if run < n:
+            tiles = [d for d in range(len(ds)) if d != u and sm[d] == hs * run and ds[d] * run >= n]
+            if len(tiles) != 1:
+                return None
+            tile = tiles[0]
+        if u in claimed or tile in claimed:
+            return None
+        claimed.add(u)
+        if tile is not None:
+            claimed.add(tile)
+        owners[j] = (u, tile, run)
+    if any(ds[d] > 1 and d not in claimed for d in range(len(ds))):
+        return None
+    return owners
+
+
+def _row_major(sizes):
+    st, run = [0] * len(sizes), 1
+    for i in range(len(sizes) - 1, -1, -1):
+        st[i] = run
+        run *= int(sizes[i])
+    return st
+
+
+def _view_box(t: SpyreTensor, allow_broadcast: bool):
+    """(host dim of each view dim -- None for size-1 dims, -1 for broadcast
+    ones --, start host coords) of a view that is a box of the geometry,
+    else None."""
+    n, hs = t._dma_size, t._dma_stride
+    big = sorted((j for j in range(len(n)) if n[j] > 1), key=lambda j: -hs[j])
+    c0, off = [0] * len(n), t.storage_offset()
+    for j in big:
+        if hs[j] <= 0:
+            return None
+        c0[j], off = divmod(off, hs[j])
+        if c0[j] >= n[j]:
+            return None
+    if off != 0:
+        return None
+    dims, used = [], set()
+    for k in range(t.dim()):
+        size, st = t.shape[k], t.stride(k)
+        if size == 1:
+            dims.append(None)
+            continue
+        if st == 0:
+            if not allow_broadcast:
+                return None
+            dims.append(-1)
+            continue
+        js = [j for j in big if hs[j] == st]
+        if len(js) != 1 or js[0] in used or c0[js[0]] + size > n[js[0]]:
+            return None
+        used.add(js[0])
+        dims.append(js[0])
+    return dims, c0
+
+
+def _box_infos(t: SpyreTensor, host: torch.Tensor, host2device: bool):
+    """DMA loop nests moving the box view t to / from the host-order tensor
+    ``host`` (t's shape, any strides), or None when t is no box of a layout
+    _dim_owners understands.  Offsets are relative to the storage starts of
+    t's buffer and of ``host``."""
+    owners = _dim_owners(t._layout, t._dma_size, t._dma_stride)
+    box = _view_box(t, allow_broadcast=not host2device)
+    if owners is None or box is None:
+        return None
+    dims, c0 = box
+    RM = _row_major(t._layout.device_size)
+
+    def dev_pos(coords):
+        p = 0
+        for j, (u, tile, run) in owners.items():
+            p += (coords[j] % run) * RM[u] + ((coords[j] // run) * RM[tile] if tile is not None else 0)
+        return p
+
+    # Per view dim: its pieces (view start, loops [(count, device stride,
+    # host stride)], host dim or None).
+    per_dim = []
+    for k, j in enumerate(dims):
+        size, hst = t.shape[k], host.stride(k)
+        if j is None:
+            continue
+        if j == -1:  # broadcast (reads only): the same device elements
+            per_dim.append([(k, 0, [(size, 0, hst)], None)])
+            continue
+        u, tile, run = owners[j]
+        a = c0[j]
+        if tile is None or a % run + size <= run:
+            per_dim.append([(k, 0, [(size, RM[u], hst)], j)])
+            continue
+        pieces = []
+        head = (-a) % run
+        if head:
+            pieces.append((k, 0, [(head, RM[u], hst)], j))
+        whole = (size - head) // run
+        if whole:
+            pieces.append((k, head, [(run, RM[u], hst), (whole, RM[tile], run * hst)], j))
+        tail = size - head - whole * run
+        if tail:
+            pieces.append((k, head + whole * run, [(tail, RM[u], hst)], j))
+        per_dim.append(pieces)
+    import itertools
+
+    infos = []
+    dbase = t._data.storage_offset()
+    for combo in itertools.product(*per_dim) if per_dim else [()]:
+        coords = list(c0)
+        hoff = host.storage_offset()
+        loops = []
+        for k, start, lps, j in combo:
+            if j is not None:
+                coords[j] = c0[j] + start
+            hoff += start * host.stride(k)
+            loops += lps
+        if not loops:
+            loops = [(1, 1, 1)]
+        if len(loops) > _lib_max_rank():
+            return None
+        loops.sort(key=lambda lp: (abs(lp[1]), abs(lp[2])))  # innermost: contiguous on the device
+        info = R._lib.StrideInfo()
+        info.rank = len(loops)
+        for q, (cnt, dst_st, host_st) in enumerate(loops):
+            info.size[q] = cnt
+            info.stride_src[q] = host_st if host2device else dst_st
+            info.stride_dst[q] = dst_st if host2device else host_st
+        dpos = dbase + dev_pos(coords)
+        info.offset_src = hoff if host2device else dpos
+        info.offset_dst = dpos if host2device else hoff
+        infos.append(info)
+    return infos
+
+
+def _lib_max_rank() -> int:
+    return R._lib.SPYRE_MAX_RANK
+
+
+def _run_infos(src: torch.Tensor, dst: torch.Tensor, infos) -> None:
+    step = R._lib.SPYRE_MAX_INFOS
+    for i in range(0, len(infos), step):
+        R.dma_copy(src, dst, infos[i:i + step])
 
 
 def _h2d_into(dst: SpyreTensor, src: torch.Tensor) -> None:
@@ -242,8 +472,16 @@ def _h2d_into(dst: SpyreTensor, src: torch.Tensor) -> None:
     if dst.is_base():
         R.h2d_into(src, dst._data, dst._layout, list(dst._dma_stride))
         return
-    # A view: the rest of the allocation keeps its values, so the whole
-    # geometry goes to host order, takes src through the view and returns.
+    if dst.numel() == 0:
+        return
+    infos = _box_infos(dst, src, host2device=True)
+    if infos is not None:  # a box: its own elements only
+        R._check_layout_dtype(src.dtype, dst._layout)
+        _run_infos(src, dst._data, infos)
+        return
+    # Another view: the rest of the allocation keeps its values, so the
+    # whole geometry goes to host order, takes src through the view and
+    # returns.
     base = _d2h_base(dst)
     base.as_strided(dst.shape, dst.stride(), dst.storage_offset()).copy_(src)
     R.h2d_into(base, dst._data, dst._layout, list(dst._dma_stride))
@@ -437,12 +675,53 @@ def _restickify_op(x):
     return restickify(x)
 
 
+def _index_copy_(x, dim, index, source):
+    """x.index_copy_(dim, index, source): source's slice i goes to x's
+    slice index[i] along dim.  Runs of consecutive indices are one box
+    each, moved by its own loop nests (bytes in proportion to source), in as
+    few launches as the nests allow.  The reference serves the op as a CPU
+    fallback over the whole tensor (tests/inductor/test_inductor_ops.py:5688-5739)."""
+    if not isinstance(x, SpyreTensor):
+        raise TypeError("index_copy_ writes into a SpyreTensor")
+    dim = dim % max(1, x.dim())
+    if index.dim() > 1 or index.dtype not in (torch.int64, torch.int32):
+        raise IndexError("index_copy_(): index must be a 1-D integer tensor")
+    idx = [int(v) for v in index.reshape(-1).tolist()]
+    n = x.shape[dim] if x.dim() else 1
+    if source.dim() != x.dim() or (x.dim() and source.shape[dim] != len(idx)):
+        raise IndexError("index_copy_(): source must have the rank of self and index.numel() slices along dim")
+    for d in range(x.dim()):
+        if d != dim and source.shape[d] != x.shape[d]:
+            raise IndexError(f"index_copy_(): source and self differ in dim {d}")
+    if any(v < -n or v >= n for v in idx):
+        raise IndexError(f"index_copy_(): index out of range for dim {dim} of size {n}")
+    idx = [v % n for v in idx]
+    if source.device != x.device:
+        source = source.to(x.device)
+    if source.dtype != x.dtype:
+        source = source.to(x.dtype)
+    i = 0
+    while i < len(idx):  # a run of consecutive indices -> one box
+        j = i + 1
+        while j < len(idx) and idx[j] == idx[j - 1] + 1:
+            j += 1
+        _h2d_into(x.narrow(dim, idx[i], j - i), source.narrow(dim, i, j - i))
+        i = j
+    return x
+
+
+def _index_copy(x, dim, index, source):
+    return _index_copy_(_clone(x), dim, index, source)
+
+
 _HANDLERS = {
     aten._to_copy.default: _to_copy,
     aten.copy_.default: _copy_,
     aten.clone.default: _clone,
     aten.detach.default: _detach,
     aten.alias.default: _detach,
+    aten.index_copy_.default: _index_copy_,
+    aten.index_copy.default: _index_copy,
 }
 
 
@@ -455,4 +734,5 @@ def register_spyre_ops() -> None:
 
 __all__ = ["SpyreTensor", "spyre_empty_with_layout", "to_device_layout", "from_device_layout",
            "device_tensor_layout", "device_buffer", "copy_tensor", "set_restickify_target",
-           "restickify_target_layout", "restickify"]
+           "restickify_target_layout", "restickify", "as_strided_with_layout", "reinterpret_tensor",
+           "reinterpret_tensor_with_layout"]

@@ -16,7 +16,8 @@ an op on CPU tensors raises.  Fake kernels make the ops traceable.
   spyre::to_device_layout / spyre::from_device_layout
         Tensor.to(device_layout=) and the D2H copy on plain buffers
         (torch_spyre/_monkey_patch.py:106-155, torch_spyre/csrc/spyre_mem.cpp:594-651)
-  spyre::overwrite / overwrite_f   torch_spyre/_inductor/customops.py:260-335
+  spyre::overwrite / overwrite_f   torch_spyre/_inductor/customops.py:260-335 (overwrite_f
+                              reinplaces to overwrite under torch.compile)
   spyre::kv_append            batched paged-cache write (no reference counterpart)
   spyre::paged_decode_attention    paged split-KV decode (no reference counterpart;
                               semantics of torch_spyre/_inductor/decompositions.py:523-609)
@@ -134,6 +135,28 @@ def overwrite_f(input: torch.Tensor, output: torch.Tensor, dims: Sequence[int],
 @overwrite_f.register_fake
 def _(input, output, dims, offsets):
     return output.clone()
+
+
+# Under torch.compile, inductor's reinplace pass turns overwrite_f into an
+# in-place overwrite of its output argument (index 1) where that buffer is
+# not read afterwards, so a compiled loop of token writes does not copy the
+# cache per write: the reference's registration
+# (torch_spyre/_inductor/customops.py:333-335).
+from torch._inductor.fx_passes.reinplace import InplaceableOp, inplaceable_ops  # noqa: E402
+from torch._inductor.lowering import fallback_handler, register_lowering  # noqa: E402
+
+inplaceable_ops[torch.ops.spyre.overwrite_f.default] = InplaceableOp(torch.ops.spyre.overwrite.default, 1)
+
+
+# The reinplace pass only retargets the node; its users still read the
+# node's value.  As the reference's lowering does
+# (torch_spyre/_inductor/lowering.py:786-800), the value of an overwrite is
+# the output it wrote: the op runs as an extern kernel (the HIP relayout
+# engine) and the lowering returns that buffer.
+@register_lowering(torch.ops.spyre.overwrite.default, type_promotion_kind=None)
+def _lower_overwrite(input, output, dims, offsets):
+    fallback_handler(torch.ops.spyre.overwrite.default, add_to_fallback_set=False)(input, output, dims, offsets)
+    return output
 
 
 @torch.library.custom_op("spyre::kv_append", mutates_args=("k_cache", "v_cache"), device_types=_CUDA)
