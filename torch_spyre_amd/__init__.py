@@ -12,6 +12,7 @@ the library is not built.  There is no CPU path.
 from . import _lib
 
 _lib.lib()  # fail loudly at import when the native library is missing
+_lib.load_torch_ops()  # the C++ kernels of the attention and KV ops
 
 from .layout import (  # noqa: E402
     DataFormats,

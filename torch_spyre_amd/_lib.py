@@ -9,10 +9,18 @@ from __future__ import annotations
 
 import ctypes
 import os
+import re
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint64, c_void_p
+
+# torch first: its HIP runtime (soname libamdhip64.so.7) is then the one the
+# native libraries bind to, not a second copy from the ROCm install
+import torch
 
 LIB_NAME = "libspyre_hip.so"
 LIB_PATH = os.environ.get("SPYRE_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# The PyTorch kernels of the attention and KV ops (csrc/torch_ops.cpp),
+# linked against libspyre_hip.so beside them.
+TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libspyre_torch.so")
 
 SPYRE_OK = 0
 SPYRE_EINVAL = -1
@@ -117,6 +125,34 @@ def lib() -> ctypes.CDLL:
             raise ImportError(f"{LIB_PATH}: ABI version {handle.spyre_abi_version()} != {ABI_VERSION}")
         _lib = handle
     return _lib
+
+
+_torch_ops_loaded = False
+
+
+def load_torch_ops() -> None:
+    """Registers the spyre:: attention / KV ops and the CUDA kernel of
+    aten::_scaled_dot_product_fused_attention_overrideable (libspyre_torch.so)."""
+    global _torch_ops_loaded
+    if _torch_ops_loaded:
+        return
+    if not os.path.exists(TORCH_LIB_PATH):
+        raise ImportError(f"{TORCH_LIB_PATH} is not built; run `python torch_spyre_amd/build.py` first "
+                          "(the package has no CPU fallback)")
+    lib()
+    torch.ops.load_library(TORCH_LIB_PATH)
+    _torch_ops_loaded = True
+
+
+_OP_ERROR = re.compile(r"\[spyre_hip (\S+) (-?\d+)\] ?(.*)")
+
+
+def library_error(e: RuntimeError) -> RuntimeError:
+    """The SpyreHipError a torch op's RuntimeError carries (a failure the
+    library reported, tagged "[spyre_hip <fn> <code>]" by libspyre_torch.so),
+    else e itself."""
+    m = _OP_ERROR.search(str(e).splitlines()[0] if str(e) else "")
+    return SpyreHipError(m.group(1), int(m.group(2)), m.group(3)) if m else e
 
 
 def check(name: str, rc: int) -> None:

@@ -101,26 +101,16 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, Hkv: int, D: int)
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
               v_cache: torch.Tensor, block_table: torch.Tensor, positions: torch.Tensor) -> None:
     """Writes token positions[b] of every sequence b (k_new/v_new [B, Hkv, D])
-    into its page slot, in one launch.  positions[b] < 0 skips b."""
-    for name, t in (("k_new", k_new), ("v_new", v_new)):
-        _require_cuda(t, name)
-        if t.dtype != torch.float16 or t.dim() != 3 or not t.is_contiguous():
-            raise ValueError(f"{name} must be contiguous float16 [B, Hkv, D]")
-    B, Hkv, D = k_new.shape
-    if v_new.shape != k_new.shape:
-        raise ValueError("k_new and v_new shapes differ")
-    num_pages = _check_cache(k_cache, v_cache, Hkv, D)
-    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
-            or block_table.stride(1) != 1:
-        raise ValueError("block_table must be int32 [B, pages_per_seq] with unit column stride")
-    if positions.dtype != torch.int32 or positions.shape != (B,) or not positions.is_contiguous():
-        raise ValueError("positions must be contiguous int32 [B]")
-    rc = _lib.lib().spyre_kv_append_f16(k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(),
-                                        v_cache.data_ptr(), block_table.data_ptr(),
-                                        block_table.stride(0), block_table.shape[1],
-                                        positions.data_ptr(), B, Hkv, D,
-                                        PAGE, num_pages, _stream_ptr(k_new.device))
-    _lib.check("spyre_kv_append_f16", rc)
+    into its page slot, in one launch.  positions[b] < 0 skips b.  The C++
+    kernel of ``spyre::kv_append`` checks and launches."""
+    try:
+        _KV_APPEND(k_new, v_new, k_cache, v_cache, block_table, positions)
+    except RuntimeError as e:
+        raise _lib.library_error(e) from None
+
+
+_KV_APPEND = torch.ops.spyre.kv_append.default
+_PAGED_DECODE = torch.ops.spyre.paged_decode_attention.default
 
 
 def workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_context_len: int, split_tokens: int = 512) -> int:
@@ -179,6 +169,15 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     omitted it is read from context_lens, which synchronises).  One kernel
     when max_context_len <= CHUNK_WAVES * split_tokens, else the split pass
     then the merge pass."""
+    if workspace is None and out is None:  # the C++ kernel of spyre::paged_decode_attention
+        if scale is None:
+            scale = 1.0 / math.sqrt(q.shape[-1])
+        try:
+            o, lse = _PAGED_DECODE(q, k_cache, v_cache, block_table, context_lens, float(scale), split_tokens,
+                                   -1 if max_context_len is None else int(max_context_len))
+        except RuntimeError as e:
+            raise _lib.library_error(e) from None
+        return (o, lse) if return_lse else o
     a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
                     max_context_len, workspace)
     if out is None:
@@ -319,15 +318,15 @@ def sdpa_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     SDPA op as prefill (torch_spyre/_inductor/decompositions.py:523-609), and
     so does this: the SDPA forward kernels with Sq = 1.  Paged caches use
     ``paged_decode_attention``."""
-    from .sdpa import scaled_dot_product_attention
-
     if query.dim() != 4 or query.shape[2] != 1:
         raise ValueError("sdpa_decode handles exactly one query token: query [B, Hq, 1, D]")
-    B, Hq, _, D = query.shape
-    Bk, Hkv, S, Dk = key.shape
-    if value.shape != key.shape or Bk != B or Dk != D:
-        raise ValueError("key/value must be [B, Hkv, S, D] matching query")
-    if Hq != Hkv and not enable_gqa:
-        raise ValueError("Hq != Hkv requires enable_gqa=True")
-    return scaled_dot_product_attention(query.to(torch.float16), key.to(torch.float16), value.to(torch.float16),
-                                        scale=scale, enable_gqa=enable_gqa)
+    f16 = torch.float16
+    if query.dtype != f16 or key.dtype != f16 or value.dtype != f16:
+        query, key, value = query.to(f16), key.to(f16), value.to(f16)
+    try:  # the C++ kernel of spyre::sdpa_fwd, without the logsumexp
+        return _SDPA_FWD(query, key, value, None, False, scale, enable_gqa, False)[0]
+    except RuntimeError as e:
+        raise _lib.library_error(e) from None
+
+
+_SDPA_FWD = torch.ops.spyre.sdpa_fwd.default

@@ -25,6 +25,8 @@ an op on CPU tensors raises.  Fake kernels make the ops traceable.
   aten::_scaled_dot_product_fused_attention_overrideable (CUDA kernel)
         the reference's decomposition target (decompositions.py:523-609),
         returning its 9-tuple
+The last four are defined and implemented in C++ (csrc/torch_ops.cpp); this
+module gives them fake kernels.
 """
 
 from __future__ import annotations
@@ -33,8 +35,7 @@ from typing import Optional, Sequence
 
 import torch
 
-from . import attention, device_tensor, relayout
-from . import sdpa as _sdpa
+from . import device_tensor, relayout
 from .layout import DataFormats, SpyreTensorLayout, get_device_dtype
 
 _CUDA = ("cuda",)
@@ -159,63 +160,30 @@ def _lower_overwrite(input, output, dims, offsets):
     return output
 
 
-@torch.library.custom_op("spyre::kv_append", mutates_args=("k_cache", "v_cache"), device_types=_CUDA)
-def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-              block_table: torch.Tensor, positions: torch.Tensor) -> None:
-    attention.kv_append(k_new, v_new, k_cache, v_cache, block_table, positions)
+# spyre::kv_append, spyre::paged_decode_attention, spyre::sdpa_fwd and the
+# CUDA kernel of aten::_scaled_dot_product_fused_attention_overrideable are
+# C++ (csrc/torch_ops.cpp, loaded from libspyre_torch.so at import): they
+# check, allocate and launch without a Python frame.  Their fake kernels
+# (shapes only) make them traceable.
 
-
-@kv_append.register_fake
+@torch.library.register_fake("spyre::kv_append")
 def _(k_new, v_new, k_cache, v_cache, block_table, positions):
     return None
 
 
-@torch.library.custom_op("spyre::paged_decode_attention", mutates_args=(), device_types=_CUDA)
-def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                           block_table: torch.Tensor, context_lens: torch.Tensor, scale: float,
-                           split_tokens: int = 512, max_context_len: int = -1) -> tuple[torch.Tensor, torch.Tensor]:
-    out, lse = attention.paged_decode_attention(
-        q, k_cache, v_cache, block_table, context_lens, scale=scale, split_tokens=split_tokens,
-        max_context_len=None if max_context_len < 0 else max_context_len, return_lse=True)
-    return out, lse
-
-
-@paged_decode_attention.register_fake
+@torch.library.register_fake("spyre::paged_decode_attention")
 def _(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens=512, max_context_len=-1):
     return q.new_empty(q.shape), q.new_empty(q.shape[:2], dtype=torch.float32)
 
 
-@torch.library.custom_op("spyre::sdpa_fwd", mutates_args=(), device_types=_CUDA)
-def sdpa_fwd(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, attn_mask: Optional[torch.Tensor],
-             is_causal: bool, scale: Optional[float], enable_gqa: bool) -> tuple[torch.Tensor, torch.Tensor]:
-    """(out, lse); out has the strides of a contiguous [B, Sq, Hq, D] tensor."""
-    return _sdpa.scaled_dot_product_attention(query, key, value, attn_mask=attn_mask, is_causal=is_causal,
-                                              scale=scale, enable_gqa=enable_gqa, return_lse=True)
-
-
-@sdpa_fwd.register_fake
-def _(query, key, value, attn_mask, is_causal, scale, enable_gqa):
+@torch.library.register_fake("spyre::sdpa_fwd")
+def _(query, key, value, attn_mask=None, is_causal=False, scale=None, enable_gqa=False, return_lse=True):
     B, Hq, Sq, D = query.shape
     out = query.new_empty((B, Sq, Hq, D)).transpose(1, 2)
-    return out, query.new_empty((B, Hq, Sq), dtype=torch.float32)
+    return out, query.new_empty((B if return_lse else 0, Hq, Sq), dtype=torch.float32)
 
-
-# The reference decomposes aten::_scaled_dot_product_fused_attention_overrideable
-# for its device (torch_spyre/_inductor/decompositions.py:523-609); here the op
-# gets a CUDA kernel returning the same 9-tuple.  torch registers only a
-# CompositeExplicitAutograd kernel for it, so this one serves CUDA tensors.
-_ATEN_IMPL = torch.library.Library("aten", "IMPL")
-
-
-def _sdpa_overrideable_cuda(query, key, value, attn_bias=None, dropout_p=0.0, is_causal=False,
-                            return_debug_mask=False, *, scale=None):
-    return _sdpa.sdpa_overrideable(query, key, value, attn_bias=attn_bias, dropout_p=dropout_p,
-                                   is_causal=is_causal, return_debug_mask=return_debug_mask, scale=scale)
-
-
-_ATEN_IMPL.impl("_scaled_dot_product_fused_attention_overrideable", _sdpa_overrideable_cuda, "CUDA")
 
 device_tensor.register_spyre_ops()
 
 __all__ = ["relayout_op", "restickify", "copy_from_d2d", "to_device_layout", "from_device_layout", "overwrite",
-           "overwrite_f", "kv_append", "paged_decode_attention", "sdpa_fwd", "DataFormats"]
+           "overwrite_f", "DataFormats"]

@@ -18,7 +18,9 @@ reference's overrideable op ``aten::_scaled_dot_product_fused_attention_override
 
 A row whose keys are all masked gives zeros (torch's CPU SDPA), not the NaN
 of the reference's plain softmax.  All work runs in the HIP kernels of
-``spyre_sdpa_fwd_f16``.
+``spyre_sdpa_fwd_f16``, called by the C++ kernels of ``spyre::sdpa_fwd`` and
+of the aten op (csrc/torch_ops.cpp), or here through the C ABI by the
+prepared ``SdpaCall`` and calls given a workspace.
 """
 
 from __future__ import annotations
@@ -150,16 +152,34 @@ def _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_g
     return args, out.transpose(1, 2), lse, (q, k, v, mask, workspace)
 
 
+_SDPA_FWD = torch.ops.spyre.sdpa_fwd.default
+
+
 def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                                  attn_mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
                                  is_causal: bool = False, scale: Optional[float] = None,
                                  enable_gqa: bool = False, return_lse: bool = False,
                                  workspace: Optional[torch.Tensor] = None):
     """``F.scaled_dot_product_attention`` on fp16 CUDA tensors: query
-    [B, Hq, Sq, D], key/value [B, Hkv, Skv, D], D in {64, 128}."""
-    args, out, lse, _ = _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa,
-                                 return_lse, workspace, True)
-    _lib.check("spyre_sdpa_fwd_f16", _lib.lib().spyre_sdpa_fwd_f16(*args, _stream_ptr(query.device)))
+    [B, Hq, Sq, D], key/value [B, Hkv, Skv, D], D in {64, 128}.
+
+    Runs the C++ kernel of ``spyre::sdpa_fwd`` (checks, outputs and the
+    call's workspace from the caching allocator, launch on the current
+    stream); with a ``workspace`` of the caller's, the library call is made
+    here with that workspace."""
+    if dropout_p > 0.0:
+        raise Unsupported("Attention dropout not implemented")
+    if workspace is not None:
+        args, out, lse, _ = _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa,
+                                     return_lse, workspace, True)
+        _lib.check("spyre_sdpa_fwd_f16", _lib.lib().spyre_sdpa_fwd_f16(*args, _stream_ptr(query.device)))
+        return (out, lse) if return_lse else out
+    if attn_mask is not None and not isinstance(attn_mask, torch.Tensor):
+        attn_mask = torch.as_tensor(attn_mask, device=query.device)
+    try:
+        out, lse = _SDPA_FWD(query, key, value, attn_mask, is_causal, scale, enable_gqa, return_lse)
+    except RuntimeError as e:
+        raise _lib.library_error(e) from None
     return (out, lse) if return_lse else out
 
 
@@ -196,13 +216,17 @@ def sdpa_overrideable(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
     """The 9-tuple of ``_scaled_dot_product_fused_attention_overrideable``
     (torch_spyre/_inductor/decompositions.py:523-609): (output, logsumexp,
     cum_seq_q, cum_seq_k, max_q, max_k, philox_seed, philox_offset,
-    debug_attn_mask).  GQA follows from the head counts."""
-    out, lse = scaled_dot_product_attention(query, key, value, attn_mask=attn_bias, dropout_p=dropout_p,
-                                            is_causal=is_causal, scale=scale,
-                                            enable_gqa=query.shape[1] != key.shape[1], return_lse=True)
-    seed = torch.empty((1,), dtype=torch.float16, device=query.device)
-    offset = torch.empty((1,), dtype=torch.float16, device=query.device)
-    return out, lse, None, None, query.shape[2], key.shape[2], seed, offset, None
+    debug_attn_mask), from the op's CUDA kernel.  GQA follows from the head
+    counts; dropout raises ``Unsupported`` as the reference does."""
+    if dropout_p > 0.0:
+        raise Unsupported("Attention dropout not implemented")
+    try:
+        return _OVERRIDEABLE(query, key, value, attn_bias, dropout_p, is_causal, return_debug_mask, scale=scale)
+    except RuntimeError as e:
+        raise _lib.library_error(e) from None
+
+
+_OVERRIDEABLE = torch.ops.aten._scaled_dot_product_fused_attention_overrideable.default
 
 
 class sdpa_override(torch.overrides.TorchFunctionMode):
