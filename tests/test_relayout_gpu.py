@@ -485,3 +485,26 @@ def test_relayout_other_dtypes_vs_oracle(cuda, dtype, shape):
     assert np.array_equal(got[:want.size], want)
     back = dev.cpu()
     assert torch.equal(back.view(raw.dtype).reshape(-1), raw)
+
+
+@pytest.mark.parametrize("nbytes,off_s,off_d", [(32 << 20, 0, 0), ((5 << 17) + 48, 0, 0), ((3 << 17) + 16, 64, 16),
+                                                (1 << 17, 8, 8), ((1 << 17) - 16, 0, 0), (48, 0, 0)])
+def test_contiguous_copy_blocks(cuda, nbytes, off_s, off_d):
+    """One contiguous nest (the byte-for-byte copy of an allocation): whole
+    128 KiB blocks through LDS, the tail by the vector kernel; offsets that
+    keep 16-byte alignment; shorter copies wholly by the vector kernel.
+    Bit-exact, and nothing outside the copy is written."""
+    import torch_spyre_amd as tsa
+
+    n = nbytes // 2
+    bits = OR.random_finite_f16_bits((n + off_s // 2,), SEED + 500 + nbytes % 997)
+    src = _bits_tensor(bits, cuda)
+    dst = torch.full((n + off_d // 2 + 64,), -1.0, dtype=torch.float16, device=cuda)
+    info = tsa._lib.StrideInfo()
+    info.rank, info.size[0], info.stride_src[0], info.stride_dst[0] = 1, n, 1, 1
+    info.offset_src, info.offset_dst = off_s // 2, off_d // 2
+    tsa.relayout.dma_copy(src, dst, [info])
+    got = _as_bits(dst)
+    assert np.array_equal(got[off_d // 2:off_d // 2 + n], bits[off_s // 2:])
+    minus_one = np.array([-1.0], dtype=np.float16).view(np.uint16)[0]
+    assert (got[:off_d // 2] == minus_one).all() and (got[off_d // 2 + n:] == minus_one).all()

@@ -427,6 +427,54 @@ __global__ __launch_bounds__(kThreads) void dma_stick_step_kernel(const char* __
   }
 }
 
+// A contiguous copy in 128 KiB blocks through LDS, the stick tiles' pattern
+// with the identity mapping: a workgroup's block is kBlockRuns runs of
+// kRunB bytes kPitchB apart, the kPitchB / kRunB workgroups of a region of
+// kPitchB x kBlockRuns bytes interleaving their runs (as the stick tiles'
+// 4 KiB src rows lie 8 KiB apart in a [4096, 4096] fp16 tensor).  1 KiB
+// chunks, chunk c loaded (straight into LDS) and stored by wavefront c % 4,
+// every load of the workgroup landed (barrier) before its first store: at
+// one workgroup per CU the device reads a round's blocks in one phase and
+// writes them in the next.  Measured on 32 MiB: 10.9 us, against 11.4 us
+// for one contiguous 128 KiB per workgroup and 13.2 us for the vector
+// kernel's interleaved loads and stores.
+#ifndef SPYRE_BLOCK_RUN
+#define SPYRE_BLOCK_RUN 4096
+#endif
+#ifndef SPYRE_BLOCK_PITCH
+#define SPYRE_BLOCK_PITCH 8192
+#endif
+constexpr int kBlockB = 128 * 1024;
+constexpr int kRunB = SPYRE_BLOCK_RUN, kPitchB = SPYRE_BLOCK_PITCH;
+constexpr int kBlockRuns = kBlockB / kRunB, kRegionB = kPitchB * kBlockRuns, kRegionBlocks = kPitchB / kRunB;
+static_assert(kRunB % 1024 == 0 && kPitchB % kRunB == 0, "whole 1 KiB chunks; runs tile the pitch");
+
+__global__ __launch_bounds__(kThreads) void dma_block_copy_kernel(const char* __restrict__ src_arg,
+                                                                  char* __restrict__ dst_arg) {
+  constexpr int kPer = kBlockB / 1024 / 4;  // 1 KiB chunks per wavefront
+  constexpr int kRunChunks = kRunB / 1024;
+  __shared__ __align__(16) char lds[kBlockB];
+  const int64_t base = static_cast<int64_t>(blockIdx.x / kRegionBlocks) * kRegionB +
+                       static_cast<int64_t>(blockIdx.x % kRegionBlocks) * kRunB;
+  const Rsrc rs = make_rsrc(src_arg + base, kRegionB), rd = make_rsrc(dst_arg + base, kRegionB);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t v = (threadIdx.x % 64) * 16;
+  // chunk c of the block: run c / kRunChunks, 1 KiB piece c % kRunChunks
+  auto off = [](uint32_t c) { return (c / kRunChunks) * kPitchB + (c % kRunChunks) * 1024; };
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t c = 4 * k + wave;
+    load_lds16(rs, v, off(c), lds + c * 1024);
+  }
+  wait_loads();
+  __syncthreads();
+  u32x4 r[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) r[k] = *reinterpret_cast<const u32x4*>(lds + (4 * k + wave) * 1024 + v);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) store16(rd, v, off(4 * k + wave), r[k]);
+}
+
 // A stick tile with a small side: n < 32 rows of T contiguous sticks on one
 // side (rows r_stride bytes apart), and the same n x T sticks dense on the
 // other, stick (y, x) at (y n + x) x 128 bytes.  Row-major -> sticks when a
@@ -969,6 +1017,28 @@ int run_info(const char* src, char* dst, int esz, const spyre_stride_info& info,
     };
     while (vb > esz && !fits(vb)) vb /= 2;
     if (!fits(vb)) vb = esz;
+    if (vb == 16 && outer.empty() && row >= kRegionB) {
+      // one contiguous run: whole regions of 128 KiB blocks through LDS,
+      // the tail (a multiple of 16 B) by the vector kernel
+      const int64_t regions = row / kRegionB;
+      const int64_t per_launch = (int64_t{1} << 30) / kRegionBlocks;
+      for (int64_t r0 = 0; r0 < regions; r0 += per_launch) {
+        const int64_t nr = std::min<int64_t>(regions - r0, per_launch);
+        dma_block_copy_kernel<<<dim3(static_cast<uint32_t>(nr * kRegionBlocks)), kThreads, 0, st>>>(
+            src + off_s + r0 * kRegionB, dst + off_d + r0 * kRegionB);
+        const int rc = check_launch("dma_block_copy_kernel");
+        if (rc != SPYRE_OK) return rc;
+      }
+      const int64_t done = regions * kRegionB;
+      if (done == row) return SPYRE_OK;
+      spyre_stride_info tail = info;
+      tail.rank = 1;
+      tail.size[0] = (row - done) / esz;
+      tail.stride_src[0] = tail.stride_dst[0] = 1;
+      tail.offset_src = info.offset_src + done / esz;
+      tail.offset_dst = info.offset_dst + done / esz;
+      return run_info(src, dst, esz, tail, st);
+    }
     if (vb == 16 && row == 128) {
       // stick tile: loop A continues the stick in dst, loop B in src.
       int ai = -1, bi = -1;
