@@ -417,24 +417,29 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   auto issue_v = [&](VT (&va)[VR][2], Rsrc vr) {
     if constexpr (DENSE) load_v_dense<D, true>(va, vr, lo, v_row); else load_v<D>(va, vr, lo);
   };
-  Rsrc kr, vr;
-  locate(0, kr, vr);
   f16x8 ka[4][DS];
   VT va[VR][2];
-  if (DENSE && ctx < kPage) {
-    if constexpr (DENSE) {  // the one short run
-      load_k_dense<D, false>(ka, kr, lo, k_row);
-      load_v_dense<D, false>(va, vr, lo, v_row);
+  {
+    Rsrc kr, vr;
+    locate(0, kr, vr);
+    if (DENSE && ctx < kPage) {
+      if constexpr (DENSE) {  // the one short run
+        load_k_dense<D, false>(ka, kr, lo, k_row);
+        load_v_dense<D, false>(va, vr, lo, v_row);
+      }
+    } else {
+      issue_k(ka, kr);
+      issue_v(va, vr);
     }
-  } else {
-    issue_k(ka, kr);
-    issue_v(va, vr);
   }
+  const bool bit3 = (lane & 8) != 0;
 
-  for (int it = 0; it < n_it; ++it) {
+  // Run it, whose operands are in ka / va.  (Two runs rotating through two
+  // sets of registers at D = 64, where they fit, measured slower: 46.7 ->
+  // 48.9 us for B 32 x 16 heads x 2048 tokens.)
+  auto step = [&](int it) {
     int lo_tok, valid;  // this run's own window tokens: [lo_tok, valid)
     window(it, lo_tok, valid);
-    const bool bit3 = (lane & 8) != 0;
 #pragma unroll
     for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
@@ -447,15 +452,17 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
       for (int ds = 0; ds < DS; ++ds)
         sc[jh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[jh][ds], qb[ds], sc[jh], 0, 0, 0);
     }
-    // The K registers are consumed: start the next page's K loads now, so
-    // they are in flight during this page's softmax and PV.
-    const bool more = it + 1 < n_it;
+    // The K registers are consumed: start the next run's K loads into them
+    // now, so they are in flight during this run's softmax and PV.
+    const int nx = it + 1;
+    const bool more = nx < n_it;
+    Rsrc kr, vr;
     if (more) {
-      if (!DENSE && ((it + 1) & 63) == 0) {
-        const int nx = it + 1 + lane;
-        ids = nx < n_it ? trow[nx] : 0;
+      if (!DENSE && (nx & 63) == 0) {  // the page ids of the next 64 runs
+        const int q = nx + lane;
+        ids = q < n_it ? trow[q] : 0;
       }
-      locate(it + 1, kr, vr);
+      locate(nx, kr, vr);
       issue_k(ka, kr);
     }
 
@@ -528,7 +535,9 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
           o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db][j], pb[j], o[db], 0, 0, 0);
     }
     if (more) issue_v(va, vr);
-  }
+  };
+
+  for (int it = 0; it < n_it; ++it) step(it);
   if (poisoned) l_run = NAN;  // propagates to the merged output: NaN, not a fault
   l_run += wave_xor(l_run, 16);
   l_run += wave_xor(l_run, 32);
