@@ -73,7 +73,9 @@ def timed(fn, steps, warmup, stream):
         fn(i)
     e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps  # ms per call
+    ms = e0.elapsed_time(e1) / steps  # per call
+    print(f"bench: {steps} calls timed, {ms * 1e3:.2f} us each", file=sys.stderr, flush=True)  # progress
+    return ms
 
 
 def cpu_model() -> str:

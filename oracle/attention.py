@@ -13,14 +13,17 @@ Test infrastructure only (see ``oracle/__init__.py``).
   reference returns an uninitialised tensor there, :584-586).
 * ``sdpa_cpu_fp32`` is the reference's CPU eager path that its tests compare
   against (tests/inductor/utils_inductor.py:662; tests/inductor/test_inductor_ops.py:5386-5392):
-  torch.nn.functional.scaled_dot_product_attention on fp32 CPU tensors.
+  torch.nn.functional.scaled_dot_product_attention on fp32 CPU tensors (a
+  causal call with a scale <= 0 as the explicit lower-triangular mask:
+  torch's own is_causal path gives NaN there).
 * ``gather_pages`` rebuilds per-sequence dense K/V from the paged stick
   layouts through ``oracle.layout`` (the layouts' own semantics).
 
 Parity pins (tests/test_oracle_attention.py): the fp64 restatement agrees with
 torch's CPU SDPA; closed cases: one key -> out = v; identical keys -> mean
 of v; a one-hot score limit; GQA head mapping h -> h // g equals
-repeat_interleave; the empty context gives zeros (torch's behaviour).
+repeat_interleave; the empty context gives zeros (torch's behaviour); a
+negative scale equals |scale| on negated queries, its logsumexp scipy's.
 """
 
 from __future__ import annotations
@@ -112,6 +115,12 @@ def sdpa_cpu_fp32(q, k, v, scale=None, attn_mask=None, is_causal=False) -> torch
         if attn_mask.dtype != torch.bool:
             attn_mask = attn_mask.float()
     gqa = q.shape[1] != k.shape[1]
+    if is_causal and scale is not None and scale <= 0:
+        # torch's CPU is_causal path returns NaN for a scale of 0 or below;
+        # its documented meaning, the top-left lower-triangular keep-mask,
+        # goes through the mask path, which handles both.
+        attn_mask = torch.ones(q.shape[-2], k.shape[-2], dtype=torch.bool).tril()
+        is_causal = False
     return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, is_causal=is_causal,
                                                             scale=scale, enable_gqa=gqa)
 

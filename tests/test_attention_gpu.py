@@ -28,6 +28,7 @@ def assert_close(got: torch.Tensor, ref: torch.Tensor):
     bound = ATOL + RTOL * ref.abs()
     bad = err > bound
     assert not torch.isnan(got).any(), "NaN in output"
+    assert not torch.isnan(ref).any(), "NaN in the reference"
     assert not bad.any(), f"{int(bad.sum())} elements out of tolerance; max abs err {err.max():.3e}"
 
 

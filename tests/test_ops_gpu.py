@@ -26,6 +26,7 @@ ATOL, RTOL, LSE_ATOL = 2e-3, 1e-2, 2e-3
 def assert_close(got, ref):
     got, ref = got.float().cpu(), torch.as_tensor(ref).float().cpu()
     assert got.shape == ref.shape and not torch.isnan(got).any()
+    assert not torch.isnan(ref).any(), "NaN in the reference"
     err = (got - ref).abs()
     assert not (err > ATOL + RTOL * ref.abs()).any(), f"max abs err {err.max():.3e}"
 

@@ -207,3 +207,52 @@ def test_decode_lse_equals_decomposition_lse(Hq, Hkv, S, D, scale):
         kk = k.numpy()[0][np.arange(Hq) % Hkv]  # [Hq, S, D], head h -> h % Hkv
         wrong = OA.decode_lse_fp64(q.numpy()[0, :, 0], kk, scale=scale)
         assert not np.allclose(wrong, want.reshape(-1), atol=1e-6)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_negative_scale_is_the_scale_on_negated_queries(causal):
+    """The decomposition takes sqrt(scale), so a negative scale is pinned
+    through the identity scale (q k^T) = |scale| ((-q) k^T): the fp64
+    restatement on -q with |scale| equals torch's fp64 SDPA with the negative
+    scale, and its logsumexp equals scipy's logsumexp of the scaled scores
+    (the row max of the -q scores, not of the +q ones, is what it keeps)."""
+    from scipy.special import logsumexp
+
+    s = 0.2
+    q, k, v = _rand((1, 2, 6, 64), 60), _rand((1, 2, 9, 64), 61), _rand((1, 2, 9, 64), 62)
+    # torch's is_causal path gives NaN under a negative scale; its mask path
+    # with the top-left lower triangle (is_causal's meaning) does not
+    tril = torch.ones(6, 9, dtype=torch.bool).tril() if causal else None
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=-s, attn_mask=tril)
+    got, lse = OA.sdpa_decomposition_fp64(-q.numpy(), k.numpy(), v.numpy(), scale=s, is_causal=causal,
+                                          return_lse=True)
+    assert np.allclose(got, ref.numpy(), atol=1e-12, rtol=1e-10)
+    scores = -s * (q.numpy() @ np.swapaxes(k.numpy(), -1, -2))
+    if causal:
+        scores = scores + np.triu(np.full(scores.shape[-2:], -np.inf), 1)
+    assert np.allclose(lse, logsumexp(scores, axis=-1), atol=1e-12, rtol=0)
+    _, lse_pos = OA.sdpa_decomposition_fp64(q.numpy(), k.numpy(), v.numpy(), scale=s, is_causal=causal,
+                                            return_lse=True)
+    assert not np.allclose(lse_pos, lse, atol=1e-3)
+    if not causal:  # the decode LSE applies the scale once, sign included
+        for i in range(6):
+            d = OA.decode_lse_fp64(q.numpy()[0, :, i], k.numpy()[0], scale=-s)
+            assert np.allclose(d, lse[0, :, i], atol=1e-12, rtol=0)
+    # the fp32 CPU path the GPU tests compare against: finite, and equal to
+    # the positive scale on -q through torch's own is_causal path
+    f32 = OA.sdpa_cpu_fp32(q.float(), k.float(), v.float(), scale=-s, is_causal=causal)
+    want = torch.nn.functional.scaled_dot_product_attention(-q.float(), k.float(), v.float(), scale=s,
+                                                            is_causal=causal)
+    assert not torch.isnan(f32).any()
+    assert torch.allclose(f32, want, atol=1e-6, rtol=1e-5)
+
+
+def test_zero_scale_causal_averages_the_visible_values():
+    """Scale 0 weighs every visible key alike: causal row i is the mean of
+    v[0 .. i] (torch's own is_causal path gives NaN at scale 0)."""
+    q, k, v = _rand((1, 2, 5, 64), 63), _rand((1, 2, 8, 64), 64), _rand((1, 2, 8, 64), 65)
+    got = OA.sdpa_cpu_fp32(q.float(), k.float(), v.float(), scale=0.0, is_causal=True)
+    want = torch.cumsum(v, dim=2)[:, :, :5] / torch.arange(1, 6, dtype=torch.float64)[:, None]
+    assert torch.allclose(got.double(), want, atol=1e-6)
+    _, lse = OA.sdpa_decomposition_fp64(q, k, v, scale=0.0, is_causal=True, return_lse=True)
+    assert np.allclose(lse, np.log(np.arange(1, 6)), atol=1e-12)

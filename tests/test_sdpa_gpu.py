@@ -28,6 +28,7 @@ def assert_close(got, ref):
     ref = torch.as_tensor(ref).float().cpu()
     assert got.shape == ref.shape, (got.shape, ref.shape)
     assert not torch.isnan(got).any(), "NaN in output"
+    assert not torch.isnan(ref).any(), "NaN in the reference"
     err = (got - ref).abs()
     bad = err > ATOL + RTOL * ref.abs()
     assert not bad.any(), f"{int(bad.sum())} elements out of tolerance; max abs err {err.max():.3e}"
@@ -341,11 +342,22 @@ def test_scale_applied_once(cuda):
 @pytest.mark.parametrize("scale", [0.0, -0.2])
 @pytest.mark.parametrize("causal", [False, True])
 def test_zero_and_negative_scale(cuda, scale, causal):
-    """scale 0 averages the visible values; a negative scale flips the
-    scores (the kernel folds the sign into q)."""
+    """scale 0 averages the visible values (LSE = log of their count); a
+    negative scale flips the scores (the kernel folds the sign into q): the
+    call equals the positive scale on -q bit for bit, and its LSE is the fp64
+    logsumexp of -q with |scale|."""
     q, k, v = randn((1, 4, 70, 64), SEED + 40), randn((1, 4, 90, 64), SEED + 41), randn((1, 4, 90, 64), SEED + 42)
-    assert_close(run(cuda, q, k, v, scale=scale, is_causal=causal),
-                 OA.sdpa_cpu_fp32(q, k, v, scale=scale, is_causal=causal))
+    out, lse = run(cuda, q, k, v, scale=scale, is_causal=causal, return_lse=True)
+    assert_close(out, OA.sdpa_cpu_fp32(q, k, v, scale=scale, is_causal=causal))
+    if scale == 0:
+        seen = torch.arange(1, 71).clamp(max=90) if causal else torch.full((70,), 90)
+        want = torch.log(seen.double()).expand(1, 4, 70)
+        assert np.allclose(lse.cpu().numpy(), want.numpy(), atol=LSE_ATOL, rtol=0)
+        return
+    out_n, lse_n = run(cuda, -q, k, v, scale=-scale, is_causal=causal, return_lse=True)
+    assert torch.equal(out.cpu(), out_n.cpu()) and torch.equal(lse.cpu(), lse_n.cpu())
+    _, lse64 = OA.sdpa_decomposition_fp64(-q, k, v, scale=-scale, is_causal=causal, return_lse=True)
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=1e-5)
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -456,9 +468,15 @@ def test_short_decode_rows_and_scales(cuda, B, Hq, Hkv, Sq, Skv, D, scale):
         assert bool(torch.isneginf(lse.cpu()).all())
         return
     assert_close(out, OA.sdpa_cpu_fp32(q, k, v, scale=scale))
-    if scale is None or scale > 0:  # the fp64 decomposition splits the scale as sqrt(scale) on q and k
-        _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, scale=scale, return_lse=True)
-        assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+    # the fp64 decomposition splits the scale as sqrt(scale) on q and k: a
+    # negative scale is |scale| on -q
+    sign = -1 if scale is not None and scale < 0 else 1
+    _, lse64 = OA.sdpa_decomposition_fp64(sign * q, k, v, scale=None if scale is None else abs(scale),
+                                          return_lse=True)
+    # rtol: q * scale * log2(e) is rounded to fp16 (relative 2^-11 per
+    # element) when |scale log2 e| <= 1, which alone moves an LSE of ~13 by
+    # up to ~2.3e-3 at the scale -0.3 case
+    assert np.allclose(lse.cpu().numpy(), lse64, atol=LSE_ATOL, rtol=2e-4)
 
 
 def test_argument_errors(cuda):
@@ -490,27 +508,59 @@ def test_llama3_8b_prefill_1024_causal_sampled_heads(cuda):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_bench_shape_prefill_sampled_heads(cuda, causal):
+def test_bench_shape_prefill_all_heads(cuda, causal):
     """The measured prefill shape (batch 1, 32 q / 8 KV heads, 4096 tokens,
-    D 128): three q heads from different KV groups against the oracle, LSE of
-    one head against the fp64 logsumexp, and for causal attention the closed
-    form of row 0 (it sees key 0 only: out = v[0]) on every head."""
+    D 128): every q head against the oracle, LSE of one head per KV group
+    against the fp64 logsumexp, and for causal attention the closed form of
+    row 0 (it sees key 0 only: out = v[0]) on every head."""
     S = 4096
     q = randn((1, 32, S, 128), SEED + 50)
     k = randn((1, 8, S, 128), SEED + 51)
     v = randn((1, 8, S, 128), SEED + 52)
     out, lse = run(cuda, q, k, v, is_causal=causal, enable_gqa=True, return_lse=True)
     out, lse = out.cpu(), lse.cpu()
-    for h in (0, 13, 31):
+    for h in range(32):
         kv = h // 4
         ref = OA.sdpa_cpu_fp32(q[:, h:h + 1], k[:, kv:kv + 1], v[:, kv:kv + 1], is_causal=causal)
         assert_close(out[:, h:h + 1], ref)
-    _, lse64 = OA.sdpa_decomposition_fp64(q[:, 13:14], k[:, 3:4], v[:, 3:4], is_causal=causal, return_lse=True)
-    assert np.allclose(lse[:, 13:14].numpy(), lse64, atol=LSE_ATOL, rtol=1e-5)
+    for h in (1, 6, 11, 13, 18, 23, 24, 31):
+        kv = h // 4
+        _, lse64 = OA.sdpa_decomposition_fp64(q[:, h:h + 1], k[:, kv:kv + 1], v[:, kv:kv + 1], is_causal=causal,
+                                              return_lse=True)
+        assert np.allclose(lse[:, h:h + 1].numpy(), lse64, atol=LSE_ATOL, rtol=1e-5), h
     if causal:
         first = out[0, :, 0].float()
         want = v[0, torch.arange(32) // 4, 0].float()
         assert torch.equal(first, want)
+
+
+@pytest.mark.parametrize("kind", ["f16", "bool"])
+def test_bench_shape_masked_prefill_sampled_heads(cuda, kind):
+    """The measured masked prefill: batch 1, 32 q / 8 KV heads, 4096 tokens,
+    D 128, one [4096, 4096] mask broadcast over heads -- an fp16 bias
+    ~ N(0, 1) or a boolean keep-mask (70 % kept).  Four q heads from
+    different KV groups against the oracle, LSE of two against the fp64
+    logsumexp."""
+    S = 4096
+    q = randn((1, 32, S, 128), SEED + 53)
+    k = randn((1, 8, S, 128), SEED + 54)
+    v = randn((1, 8, S, 128), SEED + 55)
+    gen = torch.Generator().manual_seed(SEED + 56)
+    if kind == "f16":
+        mask = torch.randn((S, S), generator=gen).half()
+    else:
+        mask = torch.rand((S, S), generator=gen) < 0.7
+    out, lse = run(cuda, q, k, v, attn_mask=mask, enable_gqa=True, return_lse=True)
+    out, lse = out.cpu(), lse.cpu()
+    for h in (0, 13, 22, 31):
+        kv = h // 4
+        ref = OA.sdpa_cpu_fp32(q[:, h:h + 1], k[:, kv:kv + 1], v[:, kv:kv + 1], attn_mask=mask)
+        assert_close(out[:, h:h + 1], ref)
+    for h in (5, 26):
+        kv = h // 4
+        _, lse64 = OA.sdpa_decomposition_fp64(q[:, h:h + 1], k[:, kv:kv + 1], v[:, kv:kv + 1],
+                                              attn_mask=mask.numpy(), return_lse=True)
+        assert np.allclose(lse[:, h:h + 1].numpy(), lse64, atol=LSE_ATOL, rtol=1e-5), h
 
 
 PREPARED_CASES = [
