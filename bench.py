@@ -224,6 +224,19 @@ def more_configs(tsa, dev, stream, steps, warmup, seed):
         "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
         "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb, "kernels_per_step": 1}
     del q5, kv5, calls5
+    # the same bytes at D 64 in one round of workgroups: q [16, 16, 1, 64],
+    # k/v [16, 16, 4096, 64] (256 (sequence, head) workgroups, 8 runs of 64
+    # tokens per wavefront, against 512 workgroups of 4 runs above)
+    q7 = torch.randn((16, 16, 1, 64), generator=gg, device=dev).half()
+    kv7 = [(torch.randn((16, 16, 4096, 64), generator=gg, device=dev).half(),
+            torch.randn((16, 16, 4096, 64), generator=gg, device=dev).half()) for _ in range(2)]
+    calls7 = [tsa.SdpaCall(q7, k, v) for k, v in kv7]
+    ms = timed(lambda i: calls7[i & 1](), steps, warmup, stream)
+    nb = 2 * kv7[0][0].numel() * 2 + 2 * q7.numel() * 2
+    res["dense_mha_decode_b16_h16_s4096_d64"] = {
+        "us_per_step": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+        "frac": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "algorithmic_bytes": nb, "kernels_per_step": 1}
+    del q7, kv7, calls7
     # chunked prefill: q [4, 32, 128, 128] against k/v [4, 8, 4096, 128] (keys split
     # 8 ways so the blocks fill the device, partials merged)
     q6 = torch.randn((4, HQ, 128, D), generator=gg, device=dev).half()
