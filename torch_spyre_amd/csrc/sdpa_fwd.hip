@@ -962,12 +962,12 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
       };
       if constexpr (MK == kNoMask) {
         if (edge(t)) mask_step(t, cur);
-        // Region A: the 2 DK MFMAs of S(t+1) beside P(t), computed against
-        // the running max as it stands.  The max matters only as a bound:
-        // while every lane's sum of P(t) stays <= 2^8, so does every P, and
-        // nothing moves.  Otherwise (and at a wavefront's first scores) the
-        // branch below takes the row max, rescales and redoes P(t) -- so the
-        // common step computes no max at all.
+        // Region A: the 2 DK MFMAs of S(t+1) beside P(t) of half 0, computed
+        // against the running max as it stands.  The max matters only as a
+        // bound: while every lane's sum of a half's P stays <= 2^8, so does
+        // every P, and nothing moves.  Otherwise (and at a wavefront's first
+        // scores) the branch below takes the row max, rescales and redoes
+        // P -- so the common step computes no max at all.
         nxt[0] = PRESCALED ? neg_m_tile : f32x16{};
         nxt[1] = PRESCALED ? neg_m_tile : f32x16{};
 #pragma unroll
@@ -975,32 +975,48 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
           mfma(2 * ks, qv[ks], nxt[0]);
           mfma(2 * ks + 1, qv[ks], nxt[1]);
         }
+        // P(t) of half 0 goes beside region A and P(t) of half 1 beside
+        // the PV MFMAs of half 0 (region B1), so both regions carry VALU
+        // work; each half has its own bound check.
         f16x8 p0[2], p1[2];
         float neg_m = m_run == -INFINITY ? 0.f : -m_run;
-        float ps = softmax_q(cur[0], 0, neg_m, p0[0]) + softmax_q(cur[0], 1, neg_m, p0[1]) +
-                   softmax_q(cur[1], 0, neg_m, p1[0]) + softmax_q(cur[1], 1, neg_m, p1[1]);
-        // Before the branch: otherwise the compiler moves P(t) into its
-        // fall-through path, after region A.
-        asm volatile("" : "+v"(p0[0]), "+v"(p0[1]), "+v"(p1[0]), "+v"(p1[1]), "+v"(ps));
-        interleave_mix(0, 2 * DK, 2, 2, 2);
+        float ps = softmax_q(cur[0], 0, neg_m, p0[0]) + softmax_q(cur[0], 1, neg_m, p0[1]);
+        asm volatile("" : "+v"(p0[0]), "+v"(p0[1]), "+v"(ps));
+        interleave_mix(0, 2 * DK, 1, 1, 1);
         if (__builtin_amdgcn_ballot_w64(!(ps <= 256.f) || m_run == -INFINITY) != 0) {
           rescale(cur, nxt, row_max(cur));
           neg_m = m_run == -INFINITY ? 0.f : -m_run;
-          ps = softmax_q(cur[0], 0, neg_m, p0[0]) + softmax_q(cur[0], 1, neg_m, p0[1]) +
-               softmax_q(cur[1], 0, neg_m, p1[0]) + softmax_q(cur[1], 1, neg_m, p1[1]);
+          ps = softmax_q(cur[0], 0, neg_m, p0[0]) + softmax_q(cur[0], 1, neg_m, p0[1]);
         }
         l_run += ps;
-        // Region B: O^T += V^T P^T.
+        // Region B1: the PV MFMAs of half 0 beside P(t) of half 1.
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + j * DM + dm, p0[j], o[dm]);
+        ps = softmax_q(cur[1], 0, neg_m, p1[0]) + softmax_q(cur[1], 1, neg_m, p1[1]);
+        asm volatile("" : "+v"(p1[0]), "+v"(p1[1]), "+v"(ps));
+        interleave_mix(2 * DK, 2 * DK + 2 * DM, 2, 2, 2);
+        if (__builtin_amdgcn_ballot_w64(!(ps <= 256.f)) != 0) {
+          // Half 1 holds a score above the bound: move the max to half 1's
+          // row max.  O (half 0's product included) and l are relative to
+          // the old max and scale with it.
+          float mx = -INFINITY;
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, cur[1][rr]);
+          rescale(cur, nxt, PRESCALED ? max_xor32(mx) + m_use : max_xor32(mx) * scale_abs);
+          neg_m = m_run == -INFINITY ? 0.f : -m_run;
+          ps = softmax_q(cur[1], 0, neg_m, p1[0]) + softmax_q(cur[1], 1, neg_m, p1[1]);
+        }
+        l_run += ps;
+        // Region B2: the PV MFMAs of half 1.
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int dm = 0; dm < DM; ++dm) mfma(2 * DK + 2 * DM + j * DM + dm, p1[j], o[dm]);
-        interleave_reads(2 * DK, kNF);
+        interleave_reads(2 * DK + 2 * DM, kNF);
       } else {
+
         // A mask can leave a step nothing to add: every score of the
         // wavefront's block -inf or more than 32 below its row's running
         // max, so every P rounds to 0 in fp16.  Such a step computes only
