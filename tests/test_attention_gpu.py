@@ -341,6 +341,44 @@ def test_argument_errors(cuda):
         run(cache, table, lens_t, q, cuda, split_tokens=100)
 
 
+def test_host_tensors_refused_before_any_launch(cuda):
+    """A tensor a kernel would reach through its pointer must be on the
+    call's GPU: host (CPU) tensors in those places raise before anything is
+    launched, in every entry point (the C++ operators, the ctypes calls, the
+    prepared call and the two passes)."""
+    import torch_spyre_amd as tsa
+
+    cache, table, lens_t, q = make_case(cuda, 2, 8, 2, 64, [100, 300], SEED + 30)
+    table, lens_t = table.to(cuda), lens_t.to(cuda)
+    ws_dev = torch.empty(tsa.workspace_bytes(2, 8, 2, 64, 300), dtype=torch.uint8, device=cuda)
+    ws_cpu = torch.empty(ws_dev.numel(), dtype=torch.uint8)
+    with pytest.raises(ValueError, match="context_lens"):
+        tsa.paged_decode_attention(q, cache.k, cache.v, table, lens_t.cpu(), max_context_len=300)
+    with pytest.raises(ValueError, match="block_table"):
+        tsa.paged_decode_attention(q, cache.k, cache.v, table.cpu(), lens_t, max_context_len=300)
+    with pytest.raises(ValueError, match="workspace"):
+        tsa.paged_decode_attention(q, cache.k, cache.v, table, lens_t, max_context_len=300, workspace=ws_cpu)
+    with pytest.raises(ValueError, match="context_lens"):
+        tsa.paged_decode_attention(q, cache.k, cache.v, table, lens_t.cpu(), max_context_len=300, workspace=ws_dev)
+    with pytest.raises(ValueError, match="out"):
+        tsa.paged_decode_attention(q, cache.k, cache.v, table, lens_t, max_context_len=300,
+                                   out=torch.empty(q.shape, dtype=q.dtype))
+    with pytest.raises(ValueError, match="out"):
+        tsa.PagedDecode(q, cache.k, cache.v, table, lens_t, max_context_len=300, out=torch.empty(q.shape, dtype=q.dtype))
+    with pytest.raises(ValueError, match="workspace"):
+        tsa.paged_decode_merge(lens_t, ws_cpu, torch.empty_like(q), 2, 300)
+    with pytest.raises(ValueError, match="positions"):
+        tsa.kv_append(q[:, :2].contiguous(), q[:, :2].contiguous(), cache.k, cache.v, table,
+                      torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(ValueError, match="block_table"):
+        tsa.kv_append(q[:, :2].contiguous(), q[:, :2].contiguous(), cache.k, cache.v, table.cpu(),
+                      torch.zeros(2, dtype=torch.int32, device=cuda))
+    qs = torch.zeros((1, 2, 8, 64), dtype=torch.float16, device=cuda)
+    with pytest.raises(ValueError, match="workspace"):
+        tsa.scaled_dot_product_attention(qs, qs, qs, workspace=torch.empty(1 << 20, dtype=torch.uint8))
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("lens", [[700, 64, 1999], [700, 64, 1999, 5000, 0, 2048, 2049]])
 def test_two_pass_api_equals_single_call_bitexact(cuda, lens):
     """paged_decode_split + paged_decode_merge == paged_decode_attention,

@@ -25,7 +25,7 @@ import torch
 
 from . import _lib
 from .layout import DataFormats, SpyreTensorLayout
-from .relayout import _require_cuda, _stream_ptr, h2d_buffer
+from .relayout import _require_cuda, _require_on, _stream_ptr, h2d_buffer
 
 PAGE = 64
 # Wavefronts per decode workgroup: a sequence is cut into chunks of at most
@@ -130,6 +130,11 @@ class _DecodeArgs:
         if Hq % Hkv:
             raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
         self.num_pages = _check_cache(k_cache, v_cache, Hkv, D)
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
+                        ("context_lens", context_lens)):
+            _require_on(t, q.device, name)
+        if workspace is not None:
+            _require_on(workspace, q.device, "workspace")
         if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B \
                 or block_table.stride(1) != 1 or not block_table.is_cuda:
             raise ValueError("block_table must be a CUDA int32 [B, W] tensor with unit column stride")
@@ -182,6 +187,9 @@ def paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
                     max_context_len, workspace)
     if out is None:
         out = torch.empty_like(q)
+    _require_on(out, q.device, "out")
+    if out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be contiguous and shaped like q")
     lse = torch.empty((a.B, a.Hq), dtype=torch.float32, device=q.device) if return_lse else None
     rc = _lib.lib().spyre_paged_decode_attn_f16(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
@@ -210,6 +218,9 @@ class PagedDecode:
         a = _DecodeArgs(q, k_cache, v_cache, block_table, context_lens, scale, split_tokens,
                         max_context_len, workspace)
         self.out = torch.empty_like(q) if out is None else out
+        _require_on(self.out, q.device, "out")
+        if lse is not None:
+            _require_on(lse, q.device, "lse")
         if self.out.shape != q.shape or self.out.dtype != q.dtype or not self.out.is_contiguous():
             raise ValueError("out must be contiguous and shaped like q")
         if lse is not None and (lse.dtype != torch.float32 or lse.shape != (a.B, a.Hq)):
@@ -269,6 +280,10 @@ def paged_decode_merge(context_lens: torch.Tensor, workspace: torch.Tensor, out:
     if out.dtype != torch.float16 or out.dim() != 3 or not out.is_contiguous():
         raise ValueError("out must be contiguous float16 [B, Hq, D]")
     B, Hq, D = out.shape
+    _require_on(context_lens, out.device, "context_lens")
+    _require_on(workspace, out.device, "workspace")
+    if lse is not None:
+        _require_on(lse, out.device, "lse")
     if context_lens.dtype != torch.int32 or context_lens.shape != (B,) or not context_lens.is_contiguous():
         raise ValueError("context_lens must be contiguous int32 [B]")
     if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, Hq) or not lse.is_contiguous()):

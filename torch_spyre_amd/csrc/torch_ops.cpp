@@ -129,6 +129,13 @@ sdpa_overrideable(const at::Tensor& query, const at::Tensor& key, const at::Tens
 
 constexpr int64_t kPage = 64;
 
+// t must be a CUDA tensor on `dev`: a kernel launched there reads or writes
+// it through its pointer (a host pointer would fault there).
+void require_on(const at::Tensor& t, const c10::Device& dev, const char* name) {
+  TORCH_CHECK_VALUE(t.is_cuda(), name, " must be a CUDA (HIP) tensor; there is no CPU path");
+  TORCH_CHECK_VALUE(t.device() == dev, name, " is on ", t.device(), "; the call runs on ", dev);
+}
+
 int64_t check_cache(const at::Tensor& kc, const at::Tensor& vc, int64_t Hkv, int64_t D) {
   for (const at::Tensor* t : {&kc, &vc}) {
     TORCH_CHECK_VALUE(t->is_cuda(), "caches must be CUDA (HIP) tensors");
@@ -153,6 +160,10 @@ std::tuple<at::Tensor, at::Tensor> paged_decode_attention(const at::Tensor& q, c
   const int64_t Hkv = k_cache.size(1);
   TORCH_CHECK_VALUE(Hkv > 0 && Hq % Hkv == 0, "Hq=", Hq, " is not a multiple of Hkv=", Hkv);
   const int64_t num_pages = check_cache(k_cache, v_cache, Hkv, D);
+  require_on(k_cache, q.device(), "k_cache");
+  require_on(v_cache, q.device(), "v_cache");
+  require_on(block_table, q.device(), "block_table");
+  require_on(context_lens, q.device(), "context_lens");
   TORCH_CHECK_VALUE(block_table.scalar_type() == at::kInt && block_table.dim() == 2 && block_table.size(0) == B &&
                         block_table.stride(1) == 1 && block_table.is_cuda(),
                     "block_table must be a CUDA int32 [B, W] tensor with unit column stride");
@@ -186,6 +197,11 @@ void kv_append(const at::Tensor& k_new, const at::Tensor& v_new, const at::Tenso
   TORCH_CHECK_VALUE(v_new.sizes() == k_new.sizes(), "k_new and v_new shapes differ");
   const int64_t B = k_new.size(0), Hkv = k_new.size(1), D = k_new.size(2);
   const int64_t num_pages = check_cache(k_cache, v_cache, Hkv, D);
+  require_on(v_new, k_new.device(), "v_new");
+  require_on(k_cache, k_new.device(), "k_cache");
+  require_on(v_cache, k_new.device(), "v_cache");
+  require_on(block_table, k_new.device(), "block_table");
+  require_on(positions, k_new.device(), "positions");
   TORCH_CHECK_VALUE(block_table.scalar_type() == at::kInt && block_table.dim() == 2 && block_table.size(0) == B &&
                         block_table.stride(1) == 1,
                     "block_table must be int32 [B, pages_per_seq] with unit column stride");

@@ -36,6 +36,13 @@ def _require_cuda(t: torch.Tensor, name: str) -> None:
         raise RuntimeError(f"{name} must be a CUDA (HIP) tensor; this package has no CPU path")
 
 
+def _require_on(t: torch.Tensor, device: torch.device, name: str) -> None:
+    """t must be a CUDA tensor on ``device``: a kernel launched there reads
+    or writes it through its pointer."""
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}; the call runs on {device} (no CPU path)")
+
+
 def _contiguous_strides(size: Sequence[int]) -> list[int]:
     st, run = [0] * len(size), 1
     for i in range(len(size) - 1, -1, -1):

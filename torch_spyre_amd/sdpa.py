@@ -32,7 +32,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .relayout import _require_cuda, _stream_ptr
+from .relayout import _require_cuda, _require_on, _stream_ptr
 
 MASK_NONE, MASK_F16, MASK_F32, MASK_BOOL = 0, 1, 2, 3
 _MASK_KIND = {torch.float16: MASK_F16, torch.float32: MASK_F32, torch.bool: MASK_BOOL, torch.uint8: MASK_BOOL}
@@ -112,6 +112,8 @@ def _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_g
     q = _operand(query, "query", copy_operands)
     k = _operand(key, "key", copy_operands)
     v = _operand(value, "value", copy_operands)
+    _require_on(k, q.device, "key")
+    _require_on(v, q.device, "value")
     B, Hq, Sq, D = q.shape
     Bk, Hkv, Skv, Dk = k.shape
     if v.shape != k.shape or Bk != B or Dk != D:
@@ -137,6 +139,8 @@ def _prepare(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_g
     s = 1.0 / math.sqrt(D) if scale is None else float(scale)
     out = torch.empty((B, Sq, Hq, D), dtype=torch.float16, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
+    if workspace is not None:
+        _require_on(workspace, q.device, "workspace")
     if workspace is None and need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     elif workspace is not None and need and kind != MASK_NONE:
