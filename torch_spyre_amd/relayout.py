@@ -59,6 +59,8 @@ def _storage_span(t: torch.Tensor) -> tuple[int, int]:
 
 def dma_copy(src: torch.Tensor, dst: torch.Tensor, infos, elem_bytes: Optional[int] = None) -> None:
     """Runs DMA loop nests (offsets relative to each tensor's storage start)."""
+    _require_cuda(dst, "dst")
+    _require_on(src, dst.device, "src")
     if not infos:
         return
     esz = elem_bytes or src.element_size()
@@ -77,6 +79,8 @@ class DmaCopy:
     HIP graph."""
 
     def __init__(self, src: torch.Tensor, dst: torch.Tensor, infos, elem_bytes: Optional[int] = None):
+        _require_cuda(dst, "dst")
+        _require_on(src, dst.device, "src")
         esz = elem_bytes or src.element_size()
         sp, sb = _storage_span(src)
         dp, db = _storage_span(dst)
