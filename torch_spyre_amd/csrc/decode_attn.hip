@@ -405,6 +405,16 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
       vr = page_rsrc(a.v + phys * page_elems + kvh * head_elems, head_bytes);
     }
   };
+  // Dense K / V: the wave streams its runs from a rotated start, run_of(it)
+  // (the softmax does not depend on the order).  Heads of contiguous
+  // [B, H, S, D] tensors lie a power of two apart, and without the rotation
+  // every workgroup reads the same offset of its head at the same moment:
+  // B 16 x 16 heads x 4096 tokens at D 64 took 50.2 us in run order and 44.1
+  // rotated, B 32 x 32 / 8 heads x 4096 at D 128 85.7 and 84.4 (one box).
+  // Paged runs keep their order (random page placement already spreads
+  // them; rotating measured slower there).
+  const int rot = DENSE && n_it > 1 ? static_cast<int>((static_cast<uint32_t>(b) * a.Hkv + kvh + p0 / n_it) % n_it) : 0;
+  auto run_of = [&](int it) { return it + rot < n_it ? it + rot : it + rot - n_it; };
   const LoadOffsets lo = DENSE ? LoadOffsets::dense<D>(lane, k_row, v_row) : LoadOffsets(lane);
   // Loads of a whole run (a page, or a 64-token window of dense K / V).
   auto issue_k = [&](f16x8 (&ka)[4][DS], Rsrc kr) {
@@ -421,7 +431,7 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   VT va[VR][2];
   {
     Rsrc kr, vr;
-    locate(0, kr, vr);
+    locate(run_of(0), kr, vr);
     if (DENSE && ctx < kPage) {
       if constexpr (DENSE) {  // the one short run
         load_k_dense<D, false>(ka, kr, lo, k_row);
@@ -439,7 +449,7 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   // 48.9 us for B 32 x 16 heads x 2048 tokens.)
   auto step = [&](int it) {
     int lo_tok, valid;  // this run's own window tokens: [lo_tok, valid)
-    window(it, lo_tok, valid);
+    window(run_of(it), lo_tok, valid);
 #pragma unroll
     for (int jh = 0; jh < 4; ++jh)
 #pragma unroll
@@ -462,7 +472,7 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
         const int q = nx + lane;
         ids = q < n_it ? trow[q] : 0;
       }
-      locate(nx, kr, vr);
+      locate(run_of(nx), kr, vr);
       issue_k(ka, kr);
     }
 
