@@ -731,6 +731,8 @@ DENSE_DECODE_CASES = [
     (64, 32, 8, 40, 0, 128),  # a context shorter than one run: per-lane offsets, tokens past it out of range
     (32, 16, 16, 33, 8, 64),  # D = 64, shorter than one run, K / V rows 72 features apart
     (64, 32, 8, 65, 0, 128),  # the last run a window of 64 tokens with one of its own
+    (64, 8, 8, 2048, 0, 128),  # four-wavefront items (the eight-wavefront grid takes two rounds)
+    (24, 32, 8, 5000, 0, 128),  # four-wavefront items in three chunks and the merge pass
 ]
 
 

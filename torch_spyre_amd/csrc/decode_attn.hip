@@ -560,7 +560,7 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 // and the whole workgroup writes the result: fp16 out and LSE when the
 // sequence has one chunk and out is given, else the chunk's partial (O per
 // q head and feature; m, l) into the workspace for the merge pass.
-template <int D, bool DENSE = false>
+template <int D, bool DENSE = false, int W = kWaves>
 __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int kvh, int wave,
                                          int lane) {
   constexpr int DB = D / 16;
@@ -572,19 +572,19 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
   const int cp0 = static_cast<int>(static_cast<int64_t>(c) * n_pages / nch);
   const int cp1 = static_cast<int>(static_cast<int64_t>(c + 1) * n_pages / nch);
   const int nc = cp1 - cp0;
-  const int w0 = cp0 + static_cast<int>(static_cast<int64_t>(wave) * nc / kWaves);
-  const int w1 = cp0 + static_cast<int>(static_cast<int64_t>(wave + 1) * nc / kWaves);
+  const int w0 = cp0 + static_cast<int>(static_cast<int64_t>(wave) * nc / W);
+  const int w1 = cp0 + static_cast<int>(static_cast<int64_t>(wave + 1) * nc / W);
   f32x4 o[DB];
   float m, l;
   stream_pages<D, DENSE>(a, b, kvh, w0, w1 - w0, ctx, lane, o, m, l);
   // Every wavefront's partial goes to LDS once; then each thread folds
-  // output elements over the kWaves partials, in wavefront order.  Lane
+  // output elements over the W partials, in wavefront order.  Lane
   // (col, grp) holds O^T[d = 16 db + 4 grp + v][col] in o[db][v]; a row of
   // 16 columns is padded so that the fold's reads of columns < 4 (the usual
   // group size) fall in distinct banks.
   constexpr int kColPad = 4;
-  __shared__ f32x4 s_o[kWaves][DB][4][16 + kColPad];
-  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  __shared__ f32x4 s_o[W][DB][4][16 + kColPad];
+  __shared__ float s_m[W][16], s_l[W][16];
   {
     const int col = lane & 15, grp = lane >> 4;
 #pragma unroll
@@ -598,7 +598,7 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
   const bool single = a.out && nch == 1;
   const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
   const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks + c;
-  for (int e = static_cast<int>(threadIdx.x); e < a.g * D; e += kThreads) {
+  for (int e = static_cast<int>(threadIdx.x); e < a.g * D; e += W * 64) {
     // e -> (db, grp, col, v), v fastest, then col < g, then grp.
     const int v = e & 3;
     const int r = e >> 2;
@@ -608,10 +608,10 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
     const int d = !DENSE ? 16 * db + i : D == 128 ? 8 * i + db : 8 * (i & 7) + 4 * (i >> 3) + db;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][col]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][col]);
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       // Empty partials (m = -inf) weigh 0; all empty: M = -inf, L = O = 0.
       const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
       L += s_l[w][col] * sc;
@@ -700,13 +700,35 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_split_list_ker
 }
 
 // Dense decode: item x = ((b Hkv + kvh) max_chunks + c); every sequence has
-// max_chunks chunks of its max_ctx tokens (grid = B Hkv max_chunks).
-template <int D>
-__global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_dense_kernel(SplitArgs a) {
+// max_chunks chunks of its max_ctx tokens (grid = B Hkv max_chunks).  W
+// wavefronts per item and workgroup: 8, or 4 where the eight-wavefront
+// grid would take more than one round of the device (dense_decode_plan).
+template <int D, int W = kWaves>
+__global__ __launch_bounds__(W * 64, kWavesPerSimd) void decode_dense_kernel(SplitArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const int item = blockIdx.x;
   const int c = item % a.max_chunks, r = item / a.max_chunks;
-  run_item<D, true>(a, r / a.Hkv, c, r % a.Hkv, wave, lane);
+  run_item<D, true, W>(a, r / a.Hkv, c, r % a.Hkv, wave, lane);
+}
+
+// Workgroup slots of the four-wavefront dense kernel on the current device
+// (cached per device), 0 if the runtime cannot say.
+int dense4_slots(int D) {
+  static std::atomic<int> cache[64][2];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::atomic<int>& c = cache[dev][D == 128];
+  int v = c.load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  const hipError_t e =
+      D == 128 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_dense_kernel<128, 4>, 4 * 64, 0)
+               : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_dense_kernel<64, 4>, 4 * 64, 0);
+  if (e != hipSuccess || cus <= 0 || per_cu <= 0) return 0;
+  v = cus * per_cu;
+  c.store(v, std::memory_order_relaxed);
+  return v;
 }
 
 struct MergeArgs {
@@ -997,7 +1019,16 @@ DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
   // 26.2 -> 15.1 us against the LDS kernel's key split, batch 24 x 512
   // 27.8 -> 12.8 us.
   if (2 * pairs * nc0 < slots || pairs * nc0 >= (int64_t{1} << 31)) return p;
-  p.chunk_pages = balanced_chunk_pages(pairs, Skv, kWaves * (split / kPage), slots);
+  // Four wavefronts per item, each with twice the runs, when the grid of
+  // eight-wavefront items would take more than one round of the device and
+  // the four-wavefront grid takes one (its workgroups hold half the waves,
+  // so about twice as many are resident): every wavefront then streams as
+  // long a share as in a one-round grid.
+  const int64_t slots4 = dense4_slots(D);
+  const int64_t nc4 = (static_cast<int64_t>(Skv) + 4 * split - 1) / (4 * split);
+  const int W = split == 512 && pairs * nc0 > slots && slots4 > 0 && pairs * nc4 <= slots4 ? 4 : kWaves;
+  p.waves = W;
+  p.chunk_pages = balanced_chunk_pages(pairs, Skv, W * (split / kPage), W == 4 ? static_cast<int>(slots4) : slots);
   p.chunks = chunks_of(Skv, p.chunk_pages);
   p.ws_bytes = p.chunks > 1 ? static_cast<size_t>(pairs) * p.chunks * (Hq / Hkv) * (D + 2) * sizeof(float) : 0;
   p.ok = true;
@@ -1042,10 +1073,15 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
   sa.v_ss = v_strides[2];
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(B) * Hkv * plan.chunks;
-  if (D == 128)
-    decode_dense_kernel<128><<<dim3(static_cast<unsigned>(items)), kThreads, 0, st>>>(sa);
+  const dim3 grid(static_cast<unsigned>(items));
+  if (D == 128 && plan.waves == 4)
+    decode_dense_kernel<128, 4><<<grid, 4 * 64, 0, st>>>(sa);
+  else if (D == 128)
+    decode_dense_kernel<128><<<grid, kThreads, 0, st>>>(sa);
+  else if (plan.waves == 4)
+    decode_dense_kernel<64, 4><<<grid, 4 * 64, 0, st>>>(sa);
   else
-    decode_dense_kernel<64><<<dim3(static_cast<unsigned>(items)), kThreads, 0, st>>>(sa);
+    decode_dense_kernel<64><<<grid, kThreads, 0, st>>>(sa);
   hipError_t e = hipGetLastError();
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode launch failed: %s", hipGetErrorString(e));
   if (plan.chunks == 1) return SPYRE_OK;  // every workgroup wrote its sequence's output

@@ -13,6 +13,7 @@ struct DenseDecodePlan {
   int chunk_pages = 0;  // 64-token runs per chunk (a workgroup's share of a sequence)
   int chunks = 0;       // chunks per sequence
   size_t ws_bytes = 0;  // fp32 chunk partials when chunks > 1, else 0
+  int waves = 8;        // wavefronts per item (= per workgroup): 8, or 4 (twice the runs each)
 };
 
 // The plan for q [B, Hq, 1, D] against K / V of Skv tokens: covered when
