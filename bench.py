@@ -13,18 +13,20 @@ serve a step from the previous one.
 
 Also timed: under "more_configs", the dense MHA decode call (q [1, 8, 1, 64], k/v
 [1, 8, 512, 64]; absolute µs, launch-bound; eager, and prepared once as SdpaCall), the
-Llama-3-8B decode step through SDPA
-with dense K/V (q [32, 32, 1, 128], k/v [32, 8, 4096, 128]), its batch-1 (absolute µs)
-and long-context (q [4, 64, 1, 128], k/v [4, 8, 32768, 128]) counterparts, the ragged batch (64 sequences, context
-~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV
-heads, append one token at position 131072, attend over 131073 tokens) and
-prefill SDPA, causal, full and with an fp16 / boolean [4096, 4096] mask
-(batch 1, 32 q / 8 KV heads, 4096 tokens), and for reference torch's fp16
-[8192, 8192] GEMM (the MFMA rate a plain library GEMM reaches on the box);
-under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
-transpose-restick, rotating 9 buffer pairs (576 MiB), with torch's CPU
-view/permute/contiguous of the same closed forms as its CPU baseline, and
-a KV cache of 8 sequences [8, 8, 2048, 128] to and from its default layout.
+Llama-3-8B decode step through SDPA with dense K/V (q [32, 32, 1, 128], k/v [32, 8, 4096,
+128]), its batch-1 (absolute µs) and long-context (q [4, 64, 1, 128], k/v [4, 8, 32768, 128])
+counterparts, head_dim 64 decode through SDPA (q [32, 16, 1, 64] against k/v [32, 16, 2048,
+64], and the same bytes as q [16, 16, 1, 64] against [16, 16, 4096, 64]), a chunked prefill
+(q [4, 32, 128, 128] against k/v [4, 8, 4096, 128]), the ragged batch (64 sequences, context
+~ U[128, 32768], seeded), the long-context step (batch 4, 64 q / 8 KV heads, append one
+token at position 131072, attend over 131073 tokens) and prefill SDPA, causal, full and
+with an fp16 / boolean [4096, 4096] mask (batch 1, 32 q / 8 KV heads, 4096 tokens), and for
+reference torch's fp16 [8192, 8192] GEMM (the MFMA rate a plain library GEMM reaches on the
+same device); under "relayout", fp16 [4096, 4096] -> sticks, sticks -> row-major and
+transpose-restick, rotating 9 buffer pairs (576 MiB), torch's copy and the identity copy
+through the same 128 KiB tile pattern, with torch's CPU view/permute/contiguous of the same
+closed forms as its CPU baseline, and a KV cache of 8 sequences [8, 8, 2048, 128] to and
+from its default layout.
 
 Timing: HIP events on the stream the kernels are launched on, around K
 back-to-back steps, after W warm-up steps.  GB/s = algorithmic bytes / time.
