@@ -243,8 +243,11 @@ size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
 /* The workspace one spyre_sdpa_fwd_f16 call needs (same arguments as the
  * call, less the causal flag).  Without a mask: the fp32 partials of a key
  * split, B * Hq * Sq * nsplit * (D + 2) * 4 bytes, when the call's blocks
- * would not fill the device (short query runs, few sequences, long keys);
- * a call given less (or causal) runs unsplit, same results within the SDPA
+ * would not fill the device (short query runs, few sequences, long keys),
+ * plus, when each KV head's g q heads x Sq queries fit one 32-row tile (the
+ * split then merges inside its one kernel), a 4-byte arrival flag per
+ * (sequence, KV head, split); the contents need no initialisation.  A
+ * call given less (or causal) runs unsplit, same results within the SDPA
  * tolerance, slower.  With a mask: 0 for fp16 / bool masks with
  * key stride 1, a 16-byte aligned pointer, b / h / i strides and Skv of
  * whole 16 bytes (staged in LDS beside K and V as they lie); for other fp16 / bool

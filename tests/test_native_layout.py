@@ -194,10 +194,12 @@ def test_sdpa_call_workspace_routes(tsa):
     # no mask, one row tile (g q heads x Sq <= 32 rows): the short-decode kernel takes up to
     # 8 x 64 keys per block at D 64 (batch-1 decode, 512 keys: one block per head, no
     # partials) and 8 x 32 at D 128; longer runs split into such blocks while they fit one
-    # round of the device: 4096 keys at D 128 -> 16 splits of [32 rows, 128 + 2] fp32
+    # round of the device: 4096 keys at D 128 -> 16 splits of [32 rows, 128 + 2] fp32, then a
+    # 4-byte arrival flag per (sequence, KV head, split) (the splits merge in the kernel)
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 512, 64) == 0
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 513, 64) == 8 * 2 * 66 * 4
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 4096, 128) == 32 * 16 * 130 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 513, 64) == 8 * 2 * 66 * 4 + 8 * 2 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 4096, 128) == \
+        32 * 16 * 130 * 4 + 8 * 16 * 4
     # 64 splits of 8 (sequence, KV head) blocks pass one round: the split of the LDS kernel
     # (a grid of at most an eighth of the device splits down to one 64-key step per block)
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 16384, 128) == 32 * 32 * 130 * 4

@@ -864,3 +864,44 @@ def test_dense_decode_ignores_rows_past_the_keys(cuda, D):
     for b in range(B):
         assert_close(out[b:b + 1], OA.sdpa_cpu_fp32(q[b:b + 1], kc[b:b + 1], vc[b:b + 1]))
     assert torch.isfinite(lse.cpu()).all()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Skv,D", [(1, 32, 8, 4096, 128), (1, 8, 8, 3000, 64), (2, 16, 2, 1500, 64),
+                                            (1, 4, 1, 257, 128)])
+def test_short_decode_split_merges_in_one_kernel(cuda, B, Hq, Hkv, Skv, D):
+    """A key-split short decode (one row tile per (sequence, KV head), the
+    keys over several blocks) merges inside its one kernel: the block that
+    sees every split's arrival flag combines the partials.  The prepared
+    call launches that one kernel; its workspace starts as random bytes and
+    is shared with a call of another shape between calls; forty calls in a
+    row give the same bits; outputs and LSE against the oracle."""
+    import torch_spyre_amd as tsa
+    from torch.profiler import ProfilerActivity, profile
+
+    q = randn((B, Hq, 1, D), SEED + 110 + Skv)
+    k, v = randn((B, Hkv, Skv, D), SEED + 111), randn((B, Hkv, Skv, D), SEED + 112)
+    qo, ko, vo = randn((1, 8, 1, 128), SEED + 113), randn((1, 2, 2000, 128), SEED + 114), randn((1, 2, 2000, 128), SEED + 115)
+    from torch_spyre_amd import _lib
+
+    need = max(_lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, B, Hq, Hkv, 1, Skv, D),
+               _lib.lib().spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 2, 1, 2000, 128))
+    assert need > 0
+    ws = torch.randint(0, 256, (need,), dtype=torch.uint8, generator=torch.Generator().manual_seed(SEED + 116)).to(cuda)
+    call = tsa.SdpaCall(q.to(cuda), k.to(cuda), v.to(cuda), enable_gqa=Hq != Hkv, return_lse=True, workspace=ws)
+    other = tsa.SdpaCall(qo.to(cuda), ko.to(cuda), vo.to(cuda), enable_gqa=True, workspace=ws)
+    first = [t.clone() for t in call()]
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        call()
+        torch.cuda.synchronize(cuda)
+    kernels = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    assert len(kernels) == 1 and "sdpa_decode_short_kernel" in kernels[0], kernels
+    for i in range(40):
+        if i % 10 == 0:
+            other()
+        out, lse = call()
+        assert torch.equal(out.view(torch.int16), first[0].view(torch.int16)), i
+        assert torch.equal(lse, first[1]), i
+    assert_close(first[0], OA.sdpa_cpu_fp32(q, k, v))
+    _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
+    assert np.allclose(first[1].cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
+    assert_close(other(), OA.sdpa_cpu_fp32(qo, ko, vo))

@@ -412,6 +412,9 @@ struct Fwd2Args {
   // pass combines them.  nsplit == 1: no split.
   int nsplit, split_keys;
   float* part;
+  // sdpa_decode_short_kernel's key split: this call's arrival-flag value
+  // (nonzero, a new one per call).
+  uint32_t ticket;
   uint32_t n_items;
   int xcd_remap;
   float scale_log2;
@@ -1178,7 +1181,7 @@ struct ShortLds {
   static constexpr int kNK = (kKW * kUK + 63) / 64;      // loads per K slice
   static constexpr int kNV = kKW * D / 8 / 64;           // loads per V slice (rows of D halves)
   static constexpr int kSliceB = (kNK + kNV) * 1024;     // bytes per wavefront
-  static constexpr int kFoldF = D / 2 + 2;               // per-lane floats of a partial: O^T, m, l
+  static constexpr int kFoldF = D / 2 + 4;               // per-lane record of a partial: O^T, m, l (16-byte aligned)
   static constexpr int kBytes = kWaves2 * kSliceB;
   static_assert(kKW * D / 8 % 64 == 0, "V slices must be whole loads");
   static_assert(kWaves2 * 64 * kFoldF * 4 <= kBytes, "the fold reuses the slices");
@@ -1213,6 +1216,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   const int key_end = a.nsplit > 1 ? min(a.Skv, kb0 + a.split_keys) : a.Skv;
   const int kw = kb0 + wave * KW;
   const int rows_here = min(key_end - kw, KW);  // <= 0: no key for this wavefront
+  // Q^T operand: lane (row, half) holds features 16ks + 8half .. +8; loaded
+  // first, so that scaling it waits for Q alone.
+  f16x8 qv[DK];
+  {
+    const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(qi, a.Sq - 1)) * a.q_ss + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < DK; ++ks) qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
+  }
   _Float16* slice = lds + wave * (L::kSliceB / 2);
   constexpr uint32_t kOob = 0x80000000u;
   if (rows_here > 0) {
@@ -1232,19 +1243,13 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
                  row < rows_here ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(a.v_ss) + 8 * ch) * 2 : kOob);
     }
   }
-  // Q^T operand: lane (row, half) holds features 16ks + 8half .. +8.
-  f16x8 qv[DK];
-  {
-    const _Float16* qp = a.q + b * a.q_sb + h * a.q_sh + static_cast<int64_t>(min(qi, a.Sq - 1)) * a.q_ss + 8 * half;
 #pragma unroll
-    for (int ks = 0; ks < DK; ++ks) {
-      qv[ks] = q_ok ? *reinterpret_cast<const f16x8*>(qp + 16 * ks) : f16x8{};
-      if constexpr (PRESCALED) {
+  for (int ks = 0; ks < DK; ++ks) {
+    if constexpr (PRESCALED) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qv[ks][e] = static_cast<_Float16>(static_cast<float>(qv[ks][e]) * a.scale_log2);
-      } else if (a.scale_log2 < 0.f) {
-        qv[ks] = -qv[ks];
-      }
+      for (int e = 0; e < 8; ++e) qv[ks][e] = static_cast<_Float16>(static_cast<float>(qv[ks][e]) * a.scale_log2);
+    } else if (a.scale_log2 < 0.f) {
+      qv[ks] = -qv[ks];
     }
   }
   const float scale_abs = fmaxf(fabsf(a.scale_log2), 1e-30f);
@@ -1313,65 +1318,162 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
       }
   }
 
-  // Fold: every wavefront's partial (O^T relative to m, m, l per lane) to
-  // LDS over the slices, then thread t folds lane t % 64's values k = V (t /
-  // 64) .. + V - 1 over the 8 partials in wavefront order.
+  // Fold: every wavefront's partial (O^T relative to m, then m and l) to
+  // LDS over the slices, one 16-byte aligned record per lane; lanes of
+  // padding rows (qi >= Sq: a decode tile holds g of its 32 rows) write
+  // nothing.
   __syncthreads();  // every wavefront is done with its slice
   float* rec = reinterpret_cast<float*>(lds);
   constexpr int kF = L::kFoldF;
-  {
+  if (q_ok) {
     float* mine = rec + (wave * 64 + lane) * kF;
 #pragma unroll
     for (int dm = 0; dm < DM; ++dm)
 #pragma unroll
-      for (int k = 0; k < 16; ++k) mine[dm * 16 + k] = o[dm][k];
-    mine[D / 2] = m;
-    mine[D / 2 + 1] = l;
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<f32x4*>(mine + dm * 16 + 4 * i) =
+            f32x4{o[dm][4 * i], o[dm][4 * i + 1], o[dm][4 * i + 2], o[dm][4 * i + 3]};
+    *reinterpret_cast<f32x2*>(mine + D / 2) = f32x2{m, l};
   }
   __syncthreads();
-  constexpr int V = D / 2 / kWaves2;  // values per thread
-  const int fl = threadIdx.x % 64, part = threadIdx.x / 64;
-  const int fcol = fl & 31, fhalf = fl >> 5;
-  const int fqi = fcol / pack, fh = kvh * a.g + gi * pack + (fcol - fqi * pack);
-  if (fqi >= a.Sq) return;
-  float M = -INFINITY;
+  // Thread t folds units u = t, t + 512, ... of the valid rows: row j (tile
+  // column j) = u / (D / 4), features d = 4 (u % (D / 4)) .. d + 3, over the
+  // 8 partials in wavefront order -- only units of real rows get a thread
+  // (a decode tile of g rows: g D / 4 threads), each read 16 bytes or a
+  // broadcast.  Lane (column j, half) holds value k = 16 (d / 32) + 4 (d %
+  // 32 / 8) + d % 4 of feature d, half = d / 4 % 2.
+  constexpr int D4 = D / 4;
+  const int nv = pack * a.Sq;  // valid rows: tile columns 0 .. nv - 1
+  // Key split: the block's partial of every valid row (O unnormalised
+  // relative to M, then M and the row sum) goes to the workspace, then an
+  // arrival flag; the block that sees every split's flag merges the rows
+  // itself -- one kernel per call.  Partials and flags move with
+  // device-scope (sc1) accesses: stores write through to memory and count as
+  // done only once there, loads read memory, never a stale line of another
+  // XCD's L2 -- no cache-wide write-back or invalidate (as a release /
+  // acquire fence would issue, at ~20 us a call here) is needed.
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  constexpr int kAuxDevice = 16;  // sc1: device scope
+  const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.Sq;
+  const Rsrc pr = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, kBufRange, kRsrcWord3);
+  const uint32_t ml_off = static_cast<uint32_t>(rows * a.nsplit * D * 4);  // bytes: (M, l) pairs
+  for (int u = static_cast<int>(threadIdx.x); u < nv * D4; u += kThreads2) {
+    const int j = u / D4, d = 4 * (u - j * D4);
+    const int ln = j + 32 * ((d >> 2) & 1), k = 16 * (d >> 5) + 4 * ((d >> 3) & 3);
+    f32x2 mlw[kWaves2];  // m and half 0's l of row j
+    float l1[kWaves2];   // half 1's l
+    f32x4 val[kWaves2];
 #pragma unroll
-  for (int w = 0; w < kWaves2; ++w) M = fmaxf(M, rec[(w * 64 + fl) * kF + D / 2]);
-  float wt[kWaves2], lsum = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWaves2; ++w) {
-    const float mw = rec[(w * 64 + fl) * kF + D / 2];
-    wt[w] = mw == -INFINITY ? 0.f : fast_exp2(mw - M);  // a slice without keys weighs 0
-    // the row sum over both lane halves
-    lsum += (rec[(w * 64 + fl) * kF + D / 2 + 1] + rec[(w * 64 + (fl ^ 32)) * kF + D / 2 + 1]) * wt[w];
-  }
-  float acc[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) {
-    acc[v] = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves2; ++w) acc[v] += rec[(w * 64 + fl) * kF + part * V + v] * wt[w];
-  }
-  // Value k of lane (row, half) is O^T row d = 32 (k / 16) + 8 (k % 16 / 4) + 4 half + k % 4.
-  auto d_of = [&](int k) { return 32 * (k >> 4) + 8 * ((k & 15) >> 2) + 4 * fhalf + (k & 3); };
-  if (a.nsplit > 1) {
-    const int64_t prow = ((static_cast<int64_t>(b) * a.Hq + fh) * a.Sq + fqi) * a.nsplit + sp;
-    float* po = a.part + prow * D;
-#pragma unroll
-    for (int v = 0; v < V; ++v) po[d_of(part * V + v)] = acc[v];
-    if (part == 0 && fhalf == 0) {
-      float* pml = a.part + static_cast<int64_t>(a.B) * a.Hq * a.Sq * a.nsplit * D + 2 * prow;
-      pml[0] = M;
-      pml[1] = lsum;
+    for (int w = 0; w < kWaves2; ++w) {
+      mlw[w] = *reinterpret_cast<const f32x2*>(rec + (w * 64 + j) * kF + D / 2);
+      l1[w] = rec[(w * 64 + j + 32) * kF + D / 2 + 1];
+      val[w] = *reinterpret_cast<const f32x4*>(rec + (w * 64 + ln) * kF + k);
     }
-    return;
-  }
-  _Float16* op = a.out + ((static_cast<int64_t>(b) * a.Sq + fqi) * a.Hq + fh) * D;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    float M = -INFINITY, lsum = 0.f;
 #pragma unroll
-  for (int v = 0; v < V; ++v) op[d_of(part * V + v)] = static_cast<_Float16>(acc[v] * inv);
-  if (a.lse && part == 0 && fhalf == 0)
-    a.lse[(static_cast<int64_t>(b) * a.Hq + fh) * a.Sq + fqi] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
+    for (int w = 0; w < kWaves2; ++w) M = fmaxf(M, mlw[w][0]);
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves2; ++w) {
+      const float wt = mlw[w][0] == -INFINITY ? 0.f : fast_exp2(mlw[w][0] - M);  // a slice without keys weighs 0
+      lsum += (mlw[w][1] + l1[w]) * wt;
+      acc += val[w] * wt;
+    }
+    const int jq = j / pack, jh = kvh * a.g + gi * pack + (j - jq * pack);
+    const int64_t r = (static_cast<int64_t>(b) * a.Hq + jh) * a.Sq + jq;
+    if (a.nsplit == 1) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      f16x4 rv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rv[e] = static_cast<_Float16>(acc[e] * inv);
+      *reinterpret_cast<f16x4*>(a.out + ((static_cast<int64_t>(b) * a.Sq + jq) * a.Hq + jh) * D + d) = rv;
+      if (a.lse && d == 0) a.lse[r] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
+    } else {
+      const uint32_t prow = static_cast<uint32_t>(r * a.nsplit + sp);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc), pr, (prow * D + d) * 4, 0, kAuxDevice);
+      if (d == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, f32x2{M, lsum}), pr, ml_off + prow * 8, 0,
+                                              kAuxDevice);
+    }
+  }
+  if (a.nsplit == 1) return;
+
+  // Arrival: every wavefront's partial stores done, then wavefront 0 stores
+  // the flag (this call's ticket), waits for it, and reads every split's
+  // flag of the group.  Of any two blocks, the one whose flag store finished
+  // later reads the other's flag after it, so at least one block sees all of
+  // them.  Every block that does merges the rows, to the same bits (splits
+  // in a fixed order).  Mergers clear the flags, so replays of a captured
+  // call (one ticket) start clear; a new call's ticket matches no older
+  // call's flags.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ int s_merge;
+  // The group's flags (item: its (sequence, KV head, head group) index).
+  const uint32_t fl_off = ml_off + static_cast<uint32_t>(rows * a.nsplit * 8) + item * a.nsplit * 4;
+  if (wave == 0) {
+    if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(a.ticket, pr, fl_off + sp * 4, 0, kAuxDevice);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    bool seen = true;
+    for (int s2 = lane; s2 < a.nsplit; s2 += 64)
+      seen = seen && __builtin_amdgcn_raw_buffer_load_b32(pr, fl_off + s2 * 4, 0, kAuxDevice) == a.ticket;
+    const bool all = __all(seen);
+    if (lane == 0) s_merge = all ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_merge) return;
+
+  // Merge: thread (row j, features 4 d4 .. + 3) over every split in order,
+  // G splits' loads in flight at once; splits with l = 0 (no visible key)
+  // carry no weight.
+  constexpr int RP = kThreads2 / D4, G = 16;
+  const int d4 = static_cast<int>(threadIdx.x) % D4;
+  for (int j = static_cast<int>(threadIdx.x) / D4; j < nv; j += RP) {
+    const int jq = j / pack, jh = kvh * a.g + gi * pack + (j - jq * pack);
+    const int64_t r = (static_cast<int64_t>(b) * a.Hq + jh) * a.Sq + jq;
+    const uint32_t r0 = static_cast<uint32_t>(r * a.nsplit);
+    float Mr = -INFINITY, Lr = 0.f;
+    f32x4 ac = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.nsplit; s0 += G) {
+      f32x2 ml[G];
+      f32x4 ov[G];
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) {
+        const uint32_t s2 = static_cast<uint32_t>(s0 + jj);
+        const bool in = s2 < static_cast<uint32_t>(a.nsplit);
+        ml[jj] = in ? __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, ml_off + (r0 + s2) * 8, 0,
+                                                                                      kAuxDevice))
+                    : f32x2{-INFINITY, 0.f};
+        ov[jj] = in ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    pr, ((r0 + s2) * D + 4 * d4) * 4, 0, kAuxDevice))
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      float Mn = Mr;
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj)
+        if (ml[jj][1] > 0.f) Mn = fmaxf(Mn, ml[jj][0]);
+      if (Mn == -INFINITY) continue;  // nothing visible yet
+      const float c = exp2f(Mr - Mn);  // Mr = -inf: c = 0
+      Lr *= c;
+      ac *= c;
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) {
+        if (!(ml[jj][1] > 0.f)) continue;
+        const float w = exp2f(ml[jj][0] - Mn);
+        Lr += ml[jj][1] * w;
+        ac += ov[jj] * w;
+      }
+      Mr = Mn;
+    }
+    const float inv = Lr > 0.f ? 1.f / Lr : 0.f;
+    f16x4 rv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rv[e] = static_cast<_Float16>(ac[e] * inv);
+    *reinterpret_cast<f16x4*>(a.out + ((static_cast<int64_t>(b) * a.Sq + jq) * a.Hq + jh) * D + 4 * d4) = rv;
+    if (a.lse && d4 == 0) a.lse[r] = Lr > 0.f ? (Mr + log2f(Lr)) * kLn2 : -INFINITY;
+  }
+  for (int s2 = static_cast<int>(threadIdx.x); s2 < a.nsplit; s2 += kThreads2)
+    __builtin_amdgcn_raw_buffer_store_b32(0u, pr, fl_off + s2 * 4, 0, kAuxDevice);
 }
 
 // Combines a key split's partials per (sequence, q head, query): one
@@ -1571,7 +1673,10 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
     const int per_block = kWaves2 * (D == 64 ? ShortLds<64>::kKW : ShortLds<128>::kKW);
     const int ns = std::max(1, (Skv + per_block - 1) / per_block);
     const int64_t cus = device_cus() > 0 ? device_cus() : 256;
-    const size_t pb = split_bytes(static_cast<int64_t>(B) * Hq * Sq, ns, D);
+    // the partials, then one arrival flag per (sequence, KV head, split)
+    const size_t pb = ns > 1 ? split_bytes(static_cast<int64_t>(B) * Hq * Sq, ns, D) +
+                                   static_cast<size_t>(B) * Hkv * ns * sizeof(uint32_t)
+                             : 0;
     if (static_cast<int64_t>(B) * Hkv * ns <= cus && (ns == 1 || ws_bytes >= pb)) {
       gp.pack = g;
       gp.nsplit = ns;
@@ -1963,19 +2068,26 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     f2.m_sh = m_sh;
     f2.m_sq = m_sq;
     f2.m_bytes = static_cast<uint32_t>(mp.span);
-    if (gpl.short_decode)
-      launch_short(f2, D, prescaled, st);  // one row tile, its keys all in flight at once
-    else if (mask_kind == kMaskF16)
+    if (gpl.short_decode) {
+      // One row tile, its keys all in flight at once; a key split merges in
+      // the same kernel.
+      static std::atomic<uint32_t> tickets{0};
+      uint32_t t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;
+      if (t == 0) t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;  // 0: a cleared flag
+      f2.ticket = t;
+      launch_short(f2, D, prescaled, st);
+    } else if (mask_kind == kMaskF16) {
       launch_lds<kMaskF16>(f2, D, prescaled, st);
-    else if (mask_kind == kMaskBool)
+    } else if (mask_kind == kMaskBool) {
       launch_lds<kMaskBool>(f2, D, prescaled, st);
-    else if (static_cast<int64_t>(f2.pack) * Sq <= kQB / 2)
+    } else if (static_cast<int64_t>(f2.pack) * Sq <= kQB / 2) {
       launch_lds<kNoMask, 4, true>(f2, D, prescaled, st);  // half steps: two wavefronts per row tile
-    else if (static_cast<int64_t>(f2.pack) * Sq < kQB)
+    } else if (static_cast<int64_t>(f2.pack) * Sq < kQB) {
       launch_lds<kNoMask, 4>(f2, D, prescaled, st);  // blocks with fewer rows than wavefronts can fill
-    else
+    } else {
       launch_lds<kNoMask>(f2, D, prescaled, st);
-    if (f2.nsplit > 1) {
+    }
+    if (f2.nsplit > 1 && !gpl.short_decode) {
       const hipError_t e0 = hipGetLastError();
       SPYRE_REQUIRE(e0 == hipSuccess, SPYRE_EHIP, "sdpa launch failed: %s", hipGetErrorString(e0));
       MergeArgs ma{f2.part, f2.out, f2.lse, Hq, Sq, D, f2.nsplit, static_cast<int64_t>(B) * Hq * Sq};
