@@ -1184,7 +1184,7 @@ struct ShortLds {
   static constexpr int kFoldF = D / 2 + 4;               // per-lane record of a partial: O^T, m, l (16-byte aligned)
   static constexpr int kBytes = kWaves2 * kSliceB;
   static_assert(kKW * D / 8 % 64 == 0, "V slices must be whole loads");
-  static_assert(kWaves2 * 64 * kFoldF * 4 <= kBytes, "the fold reuses the slices");
+  static_assert(64 * kFoldF * 4 <= kSliceB, "a wavefront's fold records fit its own slice");
 };
 
 template <int D, bool PRESCALED>
@@ -1319,14 +1319,14 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   }
 
   // Fold: every wavefront's partial (O^T relative to m, then m and l) to
-  // LDS over the slices, one 16-byte aligned record per lane; lanes of
-  // padding rows (qi >= Sq: a decode tile holds g of its 32 rows) write
-  // nothing.
-  __syncthreads();  // every wavefront is done with its slice
-  float* rec = reinterpret_cast<float*>(lds);
+  // LDS, one 16-byte aligned record per lane, over its own slice -- free once
+  // its P.V operands are read, so no barrier comes before the records.
+  // Lanes of padding rows (qi >= Sq: a decode tile holds g of its 32 rows)
+  // write nothing.
   constexpr int kF = L::kFoldF;
+  auto rec_of = [&](int w, int ln) { return reinterpret_cast<float*>(lds + w * (L::kSliceB / 2)) + ln * kF; };
   if (q_ok) {
-    float* mine = rec + (wave * 64 + lane) * kF;
+    float* mine = rec_of(wave, lane);
 #pragma unroll
     for (int dm = 0; dm < DM; ++dm)
 #pragma unroll
@@ -1365,9 +1365,9 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
     f32x4 val[kWaves2];
 #pragma unroll
     for (int w = 0; w < kWaves2; ++w) {
-      mlw[w] = *reinterpret_cast<const f32x2*>(rec + (w * 64 + j) * kF + D / 2);
-      l1[w] = rec[(w * 64 + j + 32) * kF + D / 2 + 1];
-      val[w] = *reinterpret_cast<const f32x4*>(rec + (w * 64 + ln) * kF + k);
+      mlw[w] = *reinterpret_cast<const f32x2*>(rec_of(w, j) + D / 2);
+      l1[w] = rec_of(w, j + 32)[D / 2 + 1];
+      val[w] = *reinterpret_cast<const f32x4*>(rec_of(w, ln) + k);
     }
     float M = -INFINITY, lsum = 0.f;
 #pragma unroll
