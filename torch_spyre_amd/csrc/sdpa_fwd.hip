@@ -1424,10 +1424,12 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   if (!s_merge) return;
 
   // Merge: thread (row j, features 4 d4 .. + 3) over every split in order,
-  // G splits' loads in flight at once; splits with l = 0 (no visible key)
-  // carry no weight.
+  // G splits' loads in flight at once, without a branch: past the last
+  // split the loads repeat it (a valid address) and, like splits with l = 0
+  // (no visible key), carry no weight.
   constexpr int RP = kThreads2 / D4, G = 16;
   const int d4 = static_cast<int>(threadIdx.x) % D4;
+  const uint32_t last = static_cast<uint32_t>(a.nsplit - 1);
   for (int j = static_cast<int>(threadIdx.x) / D4; j < nv; j += RP) {
     const int jq = j / pack, jh = kvh * a.g + gi * pack + (j - jq * pack);
     const int64_t r = (static_cast<int64_t>(b) * a.Hq + jh) * a.Sq + jq;
@@ -1439,27 +1441,24 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
       f32x4 ov[G];
 #pragma unroll
       for (int jj = 0; jj < G; ++jj) {
-        const uint32_t s2 = static_cast<uint32_t>(s0 + jj);
-        const bool in = s2 < static_cast<uint32_t>(a.nsplit);
-        ml[jj] = in ? __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, ml_off + (r0 + s2) * 8, 0,
-                                                                                      kAuxDevice))
-                    : f32x2{-INFINITY, 0.f};
-        ov[jj] = in ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    pr, ((r0 + s2) * D + 4 * d4) * 4, 0, kAuxDevice))
-                    : f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t s2 = min(static_cast<uint32_t>(s0 + jj), last);
+        ml[jj] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, ml_off + (r0 + s2) * 8, 0, kAuxDevice));
+        ov[jj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, ((r0 + s2) * D + 4 * d4) * 4, 0,
+                                                                                 kAuxDevice));
       }
+      float mv[G];  // the split's max, or -inf when it carries no weight
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) mv[jj] = s0 + jj < a.nsplit && ml[jj][1] > 0.f ? ml[jj][0] : -INFINITY;
       float Mn = Mr;
 #pragma unroll
-      for (int jj = 0; jj < G; ++jj)
-        if (ml[jj][1] > 0.f) Mn = fmaxf(Mn, ml[jj][0]);
+      for (int jj = 0; jj < G; ++jj) Mn = fmaxf(Mn, mv[jj]);
       if (Mn == -INFINITY) continue;  // nothing visible yet
-      const float c = exp2f(Mr - Mn);  // Mr = -inf: c = 0
+      const float c = fast_exp2(Mr - Mn);  // Mr = -inf: c = 0
       Lr *= c;
       ac *= c;
 #pragma unroll
       for (int jj = 0; jj < G; ++jj) {
-        if (!(ml[jj][1] > 0.f)) continue;
-        const float w = exp2f(ml[jj][0] - Mn);
+        const float w = fast_exp2(mv[jj] - Mn);  // -inf: 0
         Lr += ml[jj][1] * w;
         ac += ov[jj] * w;
       }
