@@ -194,12 +194,18 @@ def test_sdpa_call_workspace_routes(tsa):
     # no mask, one row tile (g q heads x Sq <= 32 rows): the short-decode kernel takes up to
     # 8 x 64 keys per block at D 64 (batch-1 decode, 512 keys: one block per head, no
     # partials) and 8 x 32 at D 128; longer runs split into such blocks while they fit one
-    # round of the device: 4096 keys at D 128 -> 16 splits of [32 rows, 128 + 2] fp32, then a
-    # 4-byte arrival flag per (sequence, KV head, split) (the splits merge in the kernel)
+    # round of the device, in blocks of 4 wavefronts (half the keys) when the 8-wavefront
+    # split would use at most half the compute units: 4096 keys at D 128 -> 32 splits of
+    # [32 rows, 128 + 2] fp32, then a 4-byte arrival flag per (sequence, KV head, split) (the
+    # splits merge in the kernel); 513 keys at D 64 -> 3 splits of 256
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 512, 64) == 0
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 513, 64) == 8 * 2 * 66 * 4 + 8 * 2 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 1, 513, 64) == 8 * 3 * 66 * 4 + 8 * 3 * 4
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 4096, 128) == \
-        32 * 16 * 130 * 4 + 8 * 16 * 4
+        32 * 32 * 130 * 4 + 8 * 32 * 4
+    # 16 (sequence, KV head) pairs x 9 splits of 256 keys at 8 wavefronts fill more than half
+    # the units: 8-wavefront blocks
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 2, 64, 8, 1, 2200, 128) == \
+        2 * 64 * 9 * 130 * 4 + 16 * 9 * 4
     # 64 splits of 8 (sequence, KV head) blocks pass one round: the split of the LDS kernel
     # (a grid of at most an eighth of the device splits down to one 64-key step per block)
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 16384, 128) == 32 * 32 * 130 * 4

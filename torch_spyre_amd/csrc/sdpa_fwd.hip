@@ -1169,10 +1169,11 @@ __global__ __launch_bounds__(kThreads2) void sdpa_fwd_lds_kernel(Fwd2Args a) {
 // kb + w KW .. + KW - 1 of K and V into its own LDS slice, all loads issued
 // at kernel start, and computes its partial of the rows over them (S^T =
 // K Q^T, softmax, O^T = V^T P^T as in sdpa_fwd_lds_kernel, the V^T operands
-// through transposing LDS reads).  The 8 partials are then folded in LDS:
+// through transposing LDS reads).  The W partials are then folded in LDS:
 // the call is one round of loads and one kernel.  Longer key runs are split
-// across blocks as in sdpa_fwd_lds_kernel (partials to the workspace, then
-// sdpa_split_merge_kernel).
+// across blocks, which merge inside the kernel (below).  W = 8 wavefronts,
+// or 4 when a split needs at most half the device's compute units at 8: the
+// blocks then use every unit, each loading half the keys.
 template <int D>
 struct ShortLds {
   static constexpr int kKW = D == 64 ? 64 : 32;          // keys per wavefront
@@ -1182,17 +1183,20 @@ struct ShortLds {
   static constexpr int kNV = kKW * D / 8 / 64;           // loads per V slice (rows of D halves)
   static constexpr int kSliceB = (kNK + kNV) * 1024;     // bytes per wavefront
   static constexpr int kFoldF = D / 2 + 4;               // per-lane record of a partial: O^T, m, l (16-byte aligned)
-  static constexpr int kBytes = kWaves2 * kSliceB;
   static_assert(kKW * D / 8 % 64 == 0, "V slices must be whole loads");
   static_assert(64 * kFoldF * 4 <= kSliceB, "a wavefront's fold records fit its own slice");
 };
 
-template <int D, bool PRESCALED>
-__global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a) {
+template <int D, bool PRESCALED, int W>
+__global__ __launch_bounds__(W * 64) void sdpa_decode_short_kernel(Fwd2Args a) {
   using L = ShortLds<D>;
   constexpr int DK = D / 16, DM = D / 32;
   constexpr int KW = L::kKW, MT = KW / 32;  // 32-key S^T tiles per wavefront
-  __shared__ __align__(16) _Float16 lds[L::kBytes / 2];
+  constexpr int NT = W * 64;                // threads
+  // W slices; a four-wavefront block asks for more than half a compute
+  // unit's 160 KiB, so that no unit runs two blocks while another idles.
+  constexpr int kLdsB = W * L::kSliceB > 82 * 1024 ? W * L::kSliceB : 82 * 1024;
+  __shared__ __align__(16) _Float16 lds[kLdsB / 2];
 
   // item = ((b * Hkv + kvh) * gp + gi) * nsplit + sp (one query block).
   uint32_t item = blockIdx.x;
@@ -1204,7 +1208,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   const int kvh = static_cast<int>(r % a.Hkv);
   const int b = static_cast<int>(r / a.Hkv);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
-  __builtin_assume(wave >= 0 && wave < kWaves2);
+  __builtin_assume(wave >= 0 && wave < W);
   const int col = lane & 31, half = lane >> 5;
   const int pack = a.pack;
   const int qi = col / pack;  // this lane's row: query qi, q head h
@@ -1338,7 +1342,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   __syncthreads();
   // Thread t folds units u = t, t + 512, ... of the valid rows: row j (tile
   // column j) = u / (D / 4), features d = 4 (u % (D / 4)) .. d + 3, over the
-  // 8 partials in wavefront order -- only units of real rows get a thread
+  // W partials in wavefront order -- only units of real rows get a thread
   // (a decode tile of g rows: g D / 4 threads), each read 16 bytes or a
   // broadcast.  Lane (column j, half) holds value k = 16 (d / 32) + 4 (d %
   // 32 / 8) + d % 4 of feature d, half = d / 4 % 2.
@@ -1357,24 +1361,24 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   const int64_t rows = static_cast<int64_t>(a.B) * a.Hq * a.Sq;
   const Rsrc pr = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, kBufRange, kRsrcWord3);
   const uint32_t ml_off = static_cast<uint32_t>(rows * a.nsplit * D * 4);  // bytes: (M, l) pairs
-  for (int u = static_cast<int>(threadIdx.x); u < nv * D4; u += kThreads2) {
+  for (int u = static_cast<int>(threadIdx.x); u < nv * D4; u += NT) {
     const int j = u / D4, d = 4 * (u - j * D4);
     const int ln = j + 32 * ((d >> 2) & 1), k = 16 * (d >> 5) + 4 * ((d >> 3) & 3);
-    f32x2 mlw[kWaves2];  // m and half 0's l of row j
-    float l1[kWaves2];   // half 1's l
-    f32x4 val[kWaves2];
+    f32x2 mlw[W];  // m and half 0's l of row j
+    float l1[W];   // half 1's l
+    f32x4 val[W];
 #pragma unroll
-    for (int w = 0; w < kWaves2; ++w) {
+    for (int w = 0; w < W; ++w) {
       mlw[w] = *reinterpret_cast<const f32x2*>(rec_of(w, j) + D / 2);
       l1[w] = rec_of(w, j + 32)[D / 2 + 1];
       val[w] = *reinterpret_cast<const f32x4*>(rec_of(w, ln) + k);
     }
     float M = -INFINITY, lsum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves2; ++w) M = fmaxf(M, mlw[w][0]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, mlw[w][0]);
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kWaves2; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float wt = mlw[w][0] == -INFINITY ? 0.f : fast_exp2(mlw[w][0] - M);  // a slice without keys weighs 0
       lsum += (mlw[w][1] + l1[w]) * wt;
       acc += val[w] * wt;
@@ -1427,7 +1431,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
   // G splits' loads in flight at once, without a branch: past the last
   // split the loads repeat it (a valid address) and, like splits with l = 0
   // (no visible key), carry no weight.
-  constexpr int RP = kThreads2 / D4, G = 16;
+  constexpr int RP = NT / D4, G = 16;
   const int d4 = static_cast<int>(threadIdx.x) % D4;
   const uint32_t last = static_cast<uint32_t>(a.nsplit - 1);
   for (int j = static_cast<int>(threadIdx.x) / D4; j < nv; j += RP) {
@@ -1471,7 +1475,7 @@ __global__ __launch_bounds__(kThreads2) void sdpa_decode_short_kernel(Fwd2Args a
     *reinterpret_cast<f16x4*>(a.out + ((static_cast<int64_t>(b) * a.Sq + jq) * a.Hq + jh) * D + 4 * d4) = rv;
     if (a.lse && d4 == 0) a.lse[r] = Lr > 0.f ? (Mr + log2f(Lr)) * kLn2 : -INFINITY;
   }
-  for (int s2 = static_cast<int>(threadIdx.x); s2 < a.nsplit; s2 += kThreads2)
+  for (int s2 = static_cast<int>(threadIdx.x); s2 < a.nsplit; s2 += NT)
     __builtin_amdgcn_raw_buffer_store_b32(0u, pr, fl_off + s2 * 4, 0, kAuxDevice);
 }
 
@@ -1659,6 +1663,7 @@ struct GridPlan {
   int pack = 1, nsplit = 1, split_keys = 0;
   size_t part_bytes = 0;
   bool short_decode = false;  // sdpa_decode_short_kernel
+  int waves = kWaves2;         // its wavefronts per block
 };
 
 GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, size_t ws_bytes) {
@@ -1669,9 +1674,17 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
   // rows) whose keys fit one block (kWaves2 slices), or a split of them
   // over blocks that all run in one round of the device.
   if (!causal && Sq > 0 && static_cast<int64_t>(g) * Sq <= 32) {
-    const int per_block = kWaves2 * (D == 64 ? ShortLds<64>::kKW : ShortLds<128>::kKW);
-    const int ns = std::max(1, (Skv + per_block - 1) / per_block);
+    const int kw = D == 64 ? ShortLds<64>::kKW : ShortLds<128>::kKW;
     const int64_t cus = device_cus() > 0 ? device_cus() : 256;
+    int waves = kWaves2;
+    int ns = std::max(1, (Skv + waves * kw - 1) / (waves * kw));
+    // A split over at most half the units at eight wavefronts: four-wavefront
+    // blocks of half the keys, twice as many, one per unit (batch-1 GQA, 4096
+    // keys at D 128: 256 blocks of 128 keys instead of 128 of 256).
+    if (ns > 1 && static_cast<int64_t>(B) * Hkv * 2 * ns <= cus) {
+      waves = 4;
+      ns = (Skv + waves * kw - 1) / (waves * kw);
+    }
     // the partials, then one arrival flag per (sequence, KV head, split)
     const size_t pb = ns > 1 ? split_bytes(static_cast<int64_t>(B) * Hq * Sq, ns, D) +
                                    static_cast<size_t>(B) * Hkv * ns * sizeof(uint32_t)
@@ -1679,9 +1692,10 @@ GridPlan plan_grid(int B, int Hq, int Hkv, int Sq, int Skv, int D, bool causal, 
     if (static_cast<int64_t>(B) * Hkv * ns <= cus && (ns == 1 || ws_bytes >= pb)) {
       gp.pack = g;
       gp.nsplit = ns;
-      gp.split_keys = ns > 1 ? per_block : Skv;
+      gp.split_keys = ns > 1 ? waves * kw : Skv;
       gp.part_bytes = pb;
       gp.short_decode = true;
+      gp.waves = waves;
       return gp;
     }
   }
@@ -1713,16 +1727,24 @@ spyre_hip::DenseDecodePlan dense_route(int B, int Hq, int Hkv, int Sq, int Skv, 
   return spyre_hip::dense_decode_plan(B, Hq, Hkv, Skv, D);
 }
 
-void launch_short(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
+template <int W>
+void launch_short_w(const Fwd2Args& f2, int D, bool prescaled, hipStream_t st) {
   const dim3 grid(f2.n_items);
   if (D == 128 && prescaled)
-    sdpa_decode_short_kernel<128, true><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_decode_short_kernel<128, true, W><<<grid, W * 64, 0, st>>>(f2);
   else if (D == 128)
-    sdpa_decode_short_kernel<128, false><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_decode_short_kernel<128, false, W><<<grid, W * 64, 0, st>>>(f2);
   else if (prescaled)
-    sdpa_decode_short_kernel<64, true><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_decode_short_kernel<64, true, W><<<grid, W * 64, 0, st>>>(f2);
   else
-    sdpa_decode_short_kernel<64, false><<<grid, kThreads2, 0, st>>>(f2);
+    sdpa_decode_short_kernel<64, false, W><<<grid, W * 64, 0, st>>>(f2);
+}
+
+void launch_short(const Fwd2Args& f2, int D, bool prescaled, int waves, hipStream_t st) {
+  if (waves == 4)
+    launch_short_w<4>(f2, D, prescaled, st);
+  else
+    launch_short_w<kWaves2>(f2, D, prescaled, st);
 }
 
 template <int MK, int SLOTS = 2, bool HALF = false>
@@ -2074,7 +2096,7 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
       uint32_t t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;
       if (t == 0) t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;  // 0: a cleared flag
       f2.ticket = t;
-      launch_short(f2, D, prescaled, st);
+      launch_short(f2, D, prescaled, gpl.waves, st);
     } else if (mask_kind == kMaskF16) {
       launch_lds<kMaskF16>(f2, D, prescaled, st);
     } else if (mask_kind == kMaskBool) {
