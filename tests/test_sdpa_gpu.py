@@ -867,7 +867,7 @@ def test_dense_decode_ignores_rows_past_the_keys(cuda, D):
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,Skv,D", [(1, 32, 8, 4096, 128), (1, 8, 8, 3000, 64), (2, 16, 2, 1500, 64),
-                                            (1, 4, 1, 257, 128)])
+                                            (1, 4, 1, 257, 128), (1, 32, 1, 1000, 128), (3, 32, 2, 700, 64)])
 def test_short_decode_split_merges_in_one_kernel(cuda, B, Hq, Hkv, Skv, D):
     """A key-split short decode (one row tile per (sequence, KV head), the
     keys over several blocks) merges inside its one kernel: the block that
