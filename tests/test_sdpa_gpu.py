@@ -905,3 +905,34 @@ def test_short_decode_split_merges_in_one_kernel(cuda, B, Hq, Hkv, Skv, D):
     _, lse64 = OA.sdpa_decomposition_fp64(q, k, v, return_lse=True)
     assert np.allclose(first[1].cpu().numpy(), lse64, atol=LSE_ATOL, rtol=0)
     assert_close(other(), OA.sdpa_cpu_fp32(qo, ko, vo))
+
+
+def test_short_decode_splits_on_two_streams(cuda):
+    """Two batch-1 decodes with in-kernel merges in flight at once on two
+    streams, each with its own workspace, twenty times over: every result
+    bit-equal to the same call run alone."""
+    import torch_spyre_amd as tsa
+
+    calls, refs = [], []
+    for i in range(2):
+        q = randn((1, 32, 1, 128), SEED + 120 + i).to(cuda)
+        k, v = randn((1, 8, 4096, 128), SEED + 122 + i).to(cuda), randn((1, 8, 4096, 128), SEED + 124 + i).to(cuda)
+        c = tsa.SdpaCall(q, k, v, enable_gqa=True, return_lse=True)
+        out, lse = c()
+        calls.append(c)
+        refs.append((out.clone(), lse.clone()))
+    torch.cuda.synchronize(cuda)
+    streams = [torch.cuda.Stream(device=cuda), torch.cuda.Stream(device=cuda)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(cuda))
+    got = [[], []]
+    for it in range(20):
+        for i in (0, 1):
+            with torch.cuda.stream(streams[i]):
+                out, lse = calls[i]()
+                got[i].append((out.clone(), lse.clone()))
+    torch.cuda.synchronize(cuda)
+    for i in (0, 1):
+        for it, (out, lse) in enumerate(got[i]):
+            assert torch.equal(out.view(torch.int16), refs[i][0].view(torch.int16)), (i, it)
+            assert torch.equal(lse, refs[i][1]), (i, it)
