@@ -248,7 +248,11 @@ size_t spyre_sdpa_fwd_workspace_bytes(int B, int Hkv, int Skv, int D);
  * split then merges inside its one kernel), a 4-byte arrival flag per
  * (sequence, KV head, split); the contents need no initialisation.  A
  * call given less (or causal) runs unsplit, same results within the SDPA
- * tolerance, slower.  With a mask: 0 for fp16 / bool masks with
+ * tolerance, slower.  Decode calls (Sq 1) whose (sequence, KV head, chunk)
+ * grid fills at least half the device: when a sequence spans several
+ * chunks, their fp32 partials B * Hkv * chunks * g * (D + 2) * 4 bytes and a
+ * 4-byte arrival flag per (sequence, KV head, chunk), also without
+ * initialisation (the chunks merge in the one kernel).  With a mask: 0 for fp16 / bool masks with
  * key stride 1, a 16-byte aligned pointer, b / h / i strides and Skv of
  * whole 16 bytes (staged in LDS beside K and V as they lie); for other fp16 / bool
  * masks, a copy with 16-byte rows of the mask's non-broadcast extent (then

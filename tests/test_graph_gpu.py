@@ -104,7 +104,7 @@ def test_relayout_graph_replays_match_oracle(cuda):
 def test_dense_decode_graph_replays_match_eager(cuda, B, S):
     """A prepared dense decode in a graph -- batch 1 (short-decode kernel,
     key splits + merge) and batch 4 x 8192 tokens (the split-KV decode
-    kernels, 8 chunks + merge); q and the newest key/value row rewritten
+    kernel, chunks merged in it); q and the newest key/value row rewritten
     eagerly before each replay; every replay bit-equal to the eager call."""
     import torch_spyre_amd as tsa
 

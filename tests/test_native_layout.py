@@ -206,18 +206,23 @@ def test_sdpa_call_workspace_routes(tsa):
     # the units: 8-wavefront blocks
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 2, 64, 8, 1, 2200, 128) == \
         2 * 64 * 9 * 130 * 4 + 16 * 9 * 4
-    # 64 splits of 8 (sequence, KV head) blocks pass one round: the split of the LDS kernel
-    # (a grid of at most an eighth of the device splits down to one 64-key step per block)
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 16384, 128) == 32 * 32 * 130 * 4
+    # 64 splits of 8 (sequence, KV head) blocks pass one round, so the call leaves the short
+    # kernel; the decode route then takes 32 chunks per (sequence, KV head): their partials
+    # [8, 32, 4, 128 + 2] fp32 and flags [8, 32] (above the LDS kernel's split of 32 x [32, 130])
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 32, 8, 1, 16384, 128) == \
+        8 * 32 * (4 * 130 + 1) * 4
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 1, 8, 8, 40, 127, 64) == 0  # one step
     # decode grids of at least half the device take the split-KV decode kernels on dense K / V:
     # batch 32 x 4096 tokens is one chunk per (sequence, KV head), no partials; batch 2 x 20037
-    # tokens, 16 chunks of 20 pages each: [B, Hkv, 16, g, 128 + 2] fp32
+    # tokens, 16 chunks of 20 pages each: [B, Hkv, 16, g, 128 + 2] fp32, then a 4-byte arrival
+    # flag per (sequence, KV head, chunk) (the chunks merge in the kernel)
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 32, 32, 8, 1, 4096, 128) == 0
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 2, 16, 8, 1, 20037, 128) == 2 * 8 * 16 * 2 * 130 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 2, 16, 8, 1, 20037, 128) == \
+        2 * 8 * 16 * 2 * 130 * 4 + 2 * 8 * 16 * 4
     # D 64: batch 32 x 16 heads x 2048 tokens, one chunk; batch 8 x 16384 tokens, 4 chunks of 64 + 2
     assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 32, 16, 16, 1, 2048, 64) == 0
-    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 8, 32, 8, 1, 16384, 64) == 8 * 8 * 4 * 4 * 66 * 4
+    assert L.spyre_sdpa_fwd_call_workspace_bytes(None, 0, None, 8, 32, 8, 1, 16384, 64) == \
+        8 * 8 * 4 * 4 * 66 * 4 + 8 * 8 * 4 * 4
     # staged as they lie: fp16 rows of 160 keys (320 B), bool rows of 160 B, broadcasts, wider rows
     assert need(1, [0, 0, 160, 1], 160) == 0
     assert need(3, [0, 0, 160, 1], 160) == 0

@@ -713,12 +713,12 @@ def test_key_stride_near_the_descriptor_limit(cuda, Sq):
 
 # Decode calls whose (sequence, KV head, chunk) grid fills at least half the
 # device stream dense K / V through the split-KV decode kernels: one chunk
-# per sequence, or several and the merge pass; a ragged last 64-token run
+# per sequence, or several merged in the same kernel; a ragged last 64-token run
 # (read as the 64-token window ending with the last key); contexts shorter
 # than one run; g = 1 and 16; K / V rows padded past D; D = 128 and 64.
 DENSE_DECODE_CASES = [
     (32, 32, 8, 4096, 0, 128),  # Llama-3-8B decode: one chunk per (sequence, KV head)
-    (4, 32, 8, 32768, 0, 128),  # long context: 8 chunks and the merge pass
+    (4, 32, 8, 32768, 0, 128),  # long context: 8 chunks merged in the kernel
     (2, 16, 8, 20037, 0, 128),  # 16 chunks, the last run 5 tokens
     (64, 64, 64, 1000, 0, 128),  # g = 1, a ragged last run
     (16, 256, 16, 2049, 64, 128),  # g = 16, K / V rows 192 features apart
@@ -726,13 +726,13 @@ DENSE_DECODE_CASES = [
     (3, 32, 8, 4096, 0, 128),  # 192 workgroups of one-page shares (three quarters of a 256-CU device)
     (24, 32, 8, 520, 0, 128),  # 192 single-chunk workgroups, a ragged last run
     (32, 32, 8, 4096, 0, 64),  # D = 64
-    (8, 32, 8, 16384, 0, 64),  # D = 64, chunks and the merge pass
+    (8, 32, 8, 16384, 0, 64),  # D = 64, chunks merged in the kernel
     (32, 16, 16, 2047, 8, 64),  # D = 64, g = 1, K / V rows 72 features apart, a ragged last run
     (64, 32, 8, 40, 0, 128),  # a context shorter than one run: per-lane offsets, tokens past it out of range
     (32, 16, 16, 33, 8, 64),  # D = 64, shorter than one run, K / V rows 72 features apart
     (64, 32, 8, 65, 0, 128),  # the last run a window of 64 tokens with one of its own
     (64, 8, 8, 2048, 0, 128),  # four-wavefront items (the eight-wavefront grid takes two rounds)
-    (24, 32, 8, 5000, 0, 128),  # four-wavefront items in three chunks and the merge pass
+    (24, 32, 8, 5000, 0, 128),  # four-wavefront items in three chunks merged in the kernel
 ]
 
 
@@ -907,16 +907,19 @@ def test_short_decode_split_merges_in_one_kernel(cuda, B, Hq, Hkv, Skv, D):
     assert_close(other(), OA.sdpa_cpu_fp32(qo, ko, vo))
 
 
-def test_short_decode_splits_on_two_streams(cuda):
-    """Two batch-1 decodes with in-kernel merges in flight at once on two
-    streams, each with its own workspace, twenty times over: every result
-    bit-equal to the same call run alone."""
+@pytest.mark.parametrize("B,S", [(1, 4096), (4, 8192)], ids=str)
+def test_decode_merges_in_kernel_on_two_streams(cuda, B, S):
+    """Two decodes whose chunk partials merge inside the kernel -- batch 1
+    (the short-decode kernel's key splits) and batch 4 x 8192 tokens (the
+    split-KV decode kernel's chunks) -- in flight at once on two streams,
+    each with its own workspace, twenty times over: every result bit-equal
+    to the same call run alone."""
     import torch_spyre_amd as tsa
 
     calls, refs = [], []
     for i in range(2):
-        q = randn((1, 32, 1, 128), SEED + 120 + i).to(cuda)
-        k, v = randn((1, 8, 4096, 128), SEED + 122 + i).to(cuda), randn((1, 8, 4096, 128), SEED + 124 + i).to(cuda)
+        q = randn((B, 32, 1, 128), SEED + 120 + i).to(cuda)
+        k, v = randn((B, 8, S, 128), SEED + 122 + i).to(cuda), randn((B, 8, S, 128), SEED + 124 + i).to(cuda)
         c = tsa.SdpaCall(q, k, v, enable_gqa=True, return_lse=True)
         out, lse = c()
         calls.append(c)

@@ -37,7 +37,9 @@
 //
 // Pass 2 (decode_merge_kernel): per (sequence, q head) with several chunks,
 // combine the chunks' partials -- the split-KV merge -- and write fp16 out
-// (+ optional LSE).
+// (+ optional LSE).  On dense K / V (decode_dense_kernel) the chunks merge
+// in pass 1 instead: the workgroup that sees every chunk's arrival flag of
+// its (sequence, KV head) combines them (merge_in_kernel).
 
 #include <hip/hip_runtime.h>
 
@@ -55,6 +57,9 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPage = 64;
 constexpr int kWaves = 8;  // wavefronts per workgroup = per work item
@@ -93,6 +98,10 @@ struct SplitArgs {
   // and these strides (elements), every sequence max_ctx tokens long; q
   // [B, Hq, D] with strides q_sb, q_sh.  block_table and ctx_lens unused.
   int64_t q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
+  // Dense K / V with several chunks per sequence: nonzero, this call's
+  // arrival-flag value (a new one per call); the chunks' partials then merge
+  // inside the kernel (run_item).  0: the merge pass combines them.
+  uint32_t ticket;
 };
 
 // Pages of a context and the number of chunks (of at most chunk_pages
@@ -555,11 +564,90 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   l_out = l_run;
 }
 
+// Dense K / V, several chunks per sequence: after its chunk's partial (a
+// device-scope store of every element) workgroup (b, c, kvh) stores an
+// arrival flag (the call's ticket) from wavefront 0, waits for it, and reads
+// the flags of every chunk of (b, kvh) with device-scope loads.  Of any two
+// workgroups, the one whose flag store finished later reads the other's
+// flag after it, so at least one sees all of them; every one that does
+// merges the g rows of (b, kvh) over the chunks in order (to the same bits)
+// and clears the flags, so replays of a captured call (one ticket) start
+// clear and a new call's ticket matches no older call's flags.  Thread
+// (row col, features 4 d4 .. + 3), 16 chunks' loads in flight at once;
+// loads past the last chunk repeat it and carry no weight.
+template <int D, int W>
+__device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int nch, int wave, int lane) {
+  constexpr int kAuxDevice = 16;  // sc1: device scope
+  constexpr int D4 = D / 4, G = 16;
+  const int64_t parts = static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks;
+  const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks;
+  const Rsrc wr = __builtin_amdgcn_make_buffer_rsrc(a.ws, 0, 0x7ffffff0, kRsrcWord3);
+  const uint32_t fl_off = static_cast<uint32_t>((parts * a.g * (D + 2) + slot0) * 4);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // every partial store of the workgroup done
+  __shared__ int s_merge;
+  if (wave == 0) {
+    if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(a.ticket, wr, fl_off + c * 4, 0, kAuxDevice);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    bool seen = true;
+    for (int s2 = lane; s2 < nch; s2 += 64)
+      seen = seen && __builtin_amdgcn_raw_buffer_load_b32(wr, fl_off + s2 * 4, 0, kAuxDevice) == a.ticket;
+    const bool all = __all(seen);
+    if (lane == 0) s_merge = all ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_merge) return;
+  const uint32_t ml_off = static_cast<uint32_t>(parts * a.g * D * 4);
+  const uint32_t last = static_cast<uint32_t>(nch - 1);
+  for (int u = static_cast<int>(threadIdx.x); u < a.g * D4; u += W * 64) {
+    const int col = u / D4, d = 4 * (u - col * D4);
+    float Mr = -INFINITY, Lr = 0.f;
+    f32x4 ac = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nch; s0 += G) {
+      f32x2 ml[G];
+      f32x4 ov[G];
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) {
+        const uint32_t s2 = min(static_cast<uint32_t>(s0 + jj), last);
+        const uint32_t part = static_cast<uint32_t>((slot0 + s2) * a.g + col);
+        ml[jj] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, ml_off + part * 8, 0, kAuxDevice));
+        ov[jj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (part * D + d) * 4, 0, kAuxDevice));
+      }
+      float mv[G];  // the chunk's max, or -inf past the last chunk
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) mv[jj] = s0 + jj < nch ? ml[jj][0] : -INFINITY;
+      float Mn = Mr;
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) Mn = fmaxf(Mn, mv[jj]);
+      const float r = fast_exp2(Mr - Mn);  // first round: exp2(-inf) = 0
+      Lr *= r;
+      ac *= r;
+#pragma unroll
+      for (int jj = 0; jj < G; ++jj) {
+        const float w = fast_exp2(mv[jj] - Mn);  // -inf: 0
+        Lr += ml[jj][1] * w;
+        ac += ov[jj] * w;
+      }
+      Mr = Mn;
+    }
+    const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
+    const float inv = 1.f / Lr;
+    f16x4 rv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rv[e] = to_f16(ac[e] * inv);
+    *reinterpret_cast<f16x4*>(a.out + row * D + d) = rv;
+    if (a.lse && d == 0) a.lse[row] = (Mr + log2f(Lr)) * kLn2;
+  }
+  for (int s2 = static_cast<int>(threadIdx.x); s2 < nch; s2 += W * 64)
+    __builtin_amdgcn_raw_buffer_store_b32(0u, wr, fl_off + s2 * 4, 0, kAuxDevice);
+}
+
 // Work item (sequence b, chunk c, KV head kvh), run by all kWaves
 // wavefronts of the workgroup.  The wavefronts' partials are combined in LDS
 // and the whole workgroup writes the result: fp16 out and LSE when the
 // sequence has one chunk and out is given, else the chunk's partial (O per
-// q head and feature; m, l) into the workspace for the merge pass.
+// q head and feature; m, l) into the workspace for the merge pass -- or, on
+// dense K / V with a ticket, for the merge in the same kernel.
 template <int D, bool DENSE = false, int W = kWaves>
 __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int kvh, int wave,
                                          int lane) {
@@ -598,6 +686,43 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
   const bool single = a.out && nch == 1;
   const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
   const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks + c;
+  if constexpr (DENSE) {
+    if (!single && a.ticket) {
+      // The chunk's partial as 16-byte device-scope stores (sc1: written
+      // through to memory; the merging workgroup may run on another XCD)
+      // of 4 consecutive features per thread, then the arrival flags.  The
+      // host keeps the workspace below 2^31 bytes for this path.
+      constexpr int D4 = D / 4;
+      const Rsrc wr = __builtin_amdgcn_make_buffer_rsrc(a.ws, 0, 0x7ffffff0, kRsrcWord3);
+      const uint32_t ml_off = static_cast<uint32_t>(static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D * 4);
+      for (int u = static_cast<int>(threadIdx.x); u < a.g * D4; u += W * 64) {
+        const int col = u / D4, d0 = 4 * (u - col * D4);
+        // Features d0 .. d0 + 3 are PV row i, 4 consecutive db (the
+        // inverse of the feature map below).
+        const int i = D == 128 ? d0 >> 3 : (d0 >> 3) + 8 * ((d0 >> 2) & 1);
+        const int db0 = D == 128 ? d0 & 7 : 0;
+        const int grp = i >> 2, v = i & 3;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][col]);
+        float L = 0.f;
+        f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
+          L += s_l[w][col] * sc;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) O[e] += s_o[w][db0 + e][grp][col][v] * sc;
+        }
+        const uint32_t part = static_cast<uint32_t>(slot * a.g + col);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), wr, (part * D + d0) * 4, 0, 16);
+        if (d0 == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), wr, ml_off + part * 8, 0, 16);
+      }
+      merge_in_kernel<D, W>(a, b, c, kvh, nch, wave, lane);
+      return;
+    }
+  }
   for (int e = static_cast<int>(threadIdx.x); e < a.g * D; e += W * 64) {
     // e -> (db, grp, col, v), v fastest, then col < g, then grp.
     const int v = e & 3;
@@ -1004,6 +1129,13 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
 
 namespace spyre_hip {
 
+uint32_t next_call_ticket() {
+  static std::atomic<uint32_t> tickets{0};
+  uint32_t t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (t == 0) t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;  // 0: a cleared flag
+  return t;
+}
+
 DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
   DenseDecodePlan p;
   if ((D != 64 && D != 128) || B <= 0 || B > 65535 || Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > kCols || Skv <= 0)
@@ -1030,7 +1162,9 @@ DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
   p.waves = W;
   p.chunk_pages = balanced_chunk_pages(pairs, Skv, W * (split / kPage), W == 4 ? static_cast<int>(slots4) : slots);
   p.chunks = chunks_of(Skv, p.chunk_pages);
-  p.ws_bytes = p.chunks > 1 ? static_cast<size_t>(pairs) * p.chunks * (Hq / Hkv) * (D + 2) * sizeof(float) : 0;
+  // Several chunks: their fp32 partials (O per q head and feature; m, l),
+  // then an arrival flag per chunk (uint32).
+  p.ws_bytes = p.chunks > 1 ? static_cast<size_t>(pairs) * p.chunks * ((Hq / Hkv) * (D + 2) + 1) * sizeof(float) : 0;
   p.ok = true;
   return p;
 }
@@ -1071,6 +1205,10 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
   sa.v_sb = v_strides[0];
   sa.v_sh = v_strides[1];
   sa.v_ss = v_strides[2];
+  // The chunks merge inside the kernel while the workspace is addressable
+  // with 32-bit offsets; past that, in the merge pass.
+  const bool fused = plan.chunks > 1 && plan.ws_bytes < (size_t{1} << 31);
+  sa.ticket = fused ? next_call_ticket() : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(B) * Hkv * plan.chunks;
   const dim3 grid(static_cast<unsigned>(items));
@@ -1084,7 +1222,7 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
     decode_dense_kernel<64><<<grid, kThreads, 0, st>>>(sa);
   hipError_t e = hipGetLastError();
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode launch failed: %s", hipGetErrorString(e));
-  if (plan.chunks == 1) return SPYRE_OK;  // every workgroup wrote its sequence's output
+  if (plan.chunks == 1 || fused) return SPYRE_OK;  // every sequence's output written
   const MergeArgs ma{sa.ws, nullptr, sa.out, lse, B, Hq, Hkv, sa.g, plan.chunks, plan.chunk_pages, Skv, 0};
   if (D == 128)
     decode_merge_kernel<128><<<dim3(Hq, B), 128, 0, st>>>(ma);

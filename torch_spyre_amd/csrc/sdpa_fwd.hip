@@ -2092,10 +2092,7 @@ extern "C" int spyre_sdpa_fwd_f16(const void* q, const int64_t* q_strides, const
     if (gpl.short_decode) {
       // One row tile, its keys all in flight at once; a key split merges in
       // the same kernel.
-      static std::atomic<uint32_t> tickets{0};
-      uint32_t t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;
-      if (t == 0) t = tickets.fetch_add(1, std::memory_order_relaxed) + 1;  // 0: a cleared flag
-      f2.ticket = t;
+      f2.ticket = spyre_hip::next_call_ticket();
       launch_short(f2, D, prescaled, gpl.waves, st);
     } else if (mask_kind == kMaskF16) {
       launch_lds<kMaskF16>(f2, D, prescaled, st);
