@@ -143,7 +143,8 @@ int spyre_kv_append_f16(const void* k_new, const void* v_new, void* k_cache, voi
 
 /* Workspace bytes needed by spyre_paged_decode_attn_f16: fp32 chunk
  * partials, B * Hkv * ceil(max_context_len / (8 * split_tokens)) * g * (D + 2)
- * floats. */
+ * floats, then a 4-byte arrival flag per (sequence, KV head, chunk).  The
+ * contents need no initialisation. */
 size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv, int D, int max_context_len,
                                                int split_tokens);
 
@@ -161,8 +162,12 @@ size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv, int D, in
  * a chunk of 8 * split_tokens, or up to a quarter more when larger chunks
  * pack the device's workgroups into fewer rounds (never more chunks than
  * the workspace formula counts).  When max_context_len <= 8 * split_tokens
- * this is one kernel and the workspace is not touched; otherwise the
- * chunks' partials are merged by a second kernel.
+ * this is one kernel and the workspace is not touched.  Otherwise each
+ * chunk's workgroup writes its partial and an arrival flag, and the one that
+ * sees every flag of its (sequence, KV head) merges the chunks in the same
+ * kernel and clears the flags -- when the work list fits one round of the
+ * device (spyre_paged_decode_attn_kernels); otherwise a second kernel
+ * merges them.  Two calls in flight at once need two workspaces.
  * Empty contexts give zeros (as torch's CPU SDPA does).  Replaces the SDPA
  * overrideable decomposition (torch_spyre/_inductor/decompositions.py:523-609)
  * selected by _fused_sdp_choice (torch_spyre/csrc/attn_utils.cpp:22-37). */
@@ -173,11 +178,19 @@ int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* 
                                 int D, int page_size, int64_t num_pages, int max_context_len,
                                 int split_tokens, float scale, void* stream);
 
+/* Kernels one spyre_paged_decode_attn_f16 call of these sizes launches on
+ * the current device: 1 when every context fits one chunk or the chunks
+ * merge inside the split kernel (its work list, B * Hkv * chunks items, fits
+ * one round of the device's workgroup slots), else 2; negative on bad
+ * sizes.  No reference counterpart (a helper for callers that account
+ * kernels per step). */
+int spyre_paged_decode_attn_kernels(int B, int Hq, int Hkv, int D, int max_context_len, int split_tokens);
+
 /* The two passes of spyre_paged_decode_attn_f16, for callers that schedule
  * them separately (same arguments and workspace; the merge pass reads what
- * the split pass wrote).  Pass 1 writes every chunk's partial (unnormalised
- * O, running max, row sum) to the workspace; pass 2 combines them into
- * out/lse.
+ * the split pass wrote, and no arrival flags are used).  Pass 1 writes
+ * every chunk's partial (unnormalised O, running max, row sum) to the
+ * workspace; pass 2 combines them into out/lse.
  * No reference counterpart: the reference's SDPA decomposition
  * (torch_spyre/_inductor/decompositions.py:523-609) has no split-KV form. */
 int spyre_paged_decode_attn_split_f16(const void* q, const void* k_cache, const void* v_cache,

@@ -400,6 +400,55 @@ def test_two_pass_api_equals_single_call_bitexact(cuda, lens):
     assert torch.equal(lse1, lse2)
 
 
+@pytest.mark.parametrize("B,kernels", [(7, 1), (40, 2)], ids=str)
+def test_chunks_merge_in_kernel_or_pass(cuda, B, kernels):
+    """Contexts of up to three 2048-token chunks (split 256).  7 sequences x
+    8 KV heads x 3 chunks fit one round of a 256-CU device's workgroups, so
+    the chunks merge inside the split kernel (one kernel); 40 sequences take
+    four rounds and the merge pass.  Both bit-equal to the two-pass API
+    (split, then the merge pass), every row against the oracle."""
+    import torch_spyre_amd as tsa
+    from torch_spyre_amd import _lib
+
+    if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
+        pytest.skip("the kernel counts assume a 256-CU device")
+    lens = ([5000, 700, 64, 4097, 2049, 1, 6000] * 6)[:B]
+    assert _lib.lib().spyre_paged_decode_attn_kernels(B, 32, 8, 128, max(lens), 256) == kernels
+    cache, table, lens_t, q = make_case(cuda, B, 32, 8, 128, lens, SEED + 43 + B)
+    t, l = table.to(cuda), lens_t.to(cuda)
+    call = tsa.PagedDecode(q, cache.k, cache.v, t, l, split_tokens=256, max_context_len=max(lens),
+                           lse=torch.empty((B, 32), dtype=torch.float32, device=cuda))
+    assert call.passes == kernels
+    one = call().clone()
+    lse1 = call.lse.clone()
+    call.split()
+    two = call.merge()
+    assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(lse1, call.lse)
+    rows = list(range(B))
+    assert_close(one, oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128)))
+
+
+@pytest.mark.parametrize("split", [512, 256])
+def test_context_past_max_gives_nan_rows(cuda, split):
+    """A context longer than max_context_len breaks the call's contract: the
+    kernel reads only max_context_len tokens of it and its rows come out NaN,
+    the others exact.  Split 512: every context one chunk (one kernel);
+    split 256: two chunks merged inside the kernel; and the two-pass API."""
+    import torch_spyre_amd as tsa
+
+    lens = [5000, 700, 3000, 64]
+    cache, table, lens_t, q = make_case(cuda, 4, 32, 8, 128, lens, SEED + 47)
+    t, l = table.to(cuda), lens_t.to(cuda)
+    out = tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=split, max_context_len=4000)
+    ws = torch.empty(tsa.workspace_bytes(4, 32, 8, 128, 4000, split), dtype=torch.uint8, device=cuda)
+    tsa.paged_decode_split(q, cache.k, cache.v, t, l, ws, split_tokens=split, max_context_len=4000)
+    two = tsa.paged_decode_merge(l, ws, torch.empty_like(q), 8, 4000, split_tokens=split)
+    for o in (out, two):
+        assert torch.isnan(o[0].float()).all()
+        assert_close(o[1:], oracle_rows(cache, table, lens_t, q, [1, 2, 3], 1 / math.sqrt(128)))
+
+
 def test_prepared_call_matches(cuda):
     """PagedDecode (validated once, launched repeatedly) == paged_decode_attention."""
     import torch_spyre_amd as tsa

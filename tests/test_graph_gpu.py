@@ -33,7 +33,8 @@ def _capture(cuda, fn):
 
 def test_decode_step_graph_replays_match_eager(cuda):
     """kv_append + PagedDecode with contexts up to 5000 tokens at split 512
-    (split and merge kernels) in one graph; each replay follows new q / new
+    (two chunks, merged inside the split kernel by arrival flags that each
+    replay sets and clears) in one graph; each replay follows new q / new
     token values written eagerly."""
     import torch_spyre_amd as tsa
 
@@ -48,7 +49,7 @@ def test_decode_step_graph_replays_match_eager(cuda):
     q_static = q.clone()
     call = tsa.PagedDecode(q_static, cache.k, cache.v, t, l, max_context_len=max(lens))
     ref = tsa.PagedDecode(q_static, cache.k, cache.v, t, l, max_context_len=max(lens))
-    assert call.passes == 2
+    assert call.passes == 1
 
     def step():
         tsa.kv_append(k_new, v_new, cache.k, cache.v, t, pos)

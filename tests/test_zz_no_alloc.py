@@ -5,9 +5,10 @@ caller-provided workspace.
 Checked through the C ABI against spyre_paged_decode_attn_f16 with a
 workspace (the same kernels, so bit-identical output and LSE) on two calls
 in a row, the second with a smaller batch and shorter contexts, both long
-enough to need the merge pass (more than 4096 tokens per chunk at split
-512), so the scratch carries the partials.  A call whose partials exceed
-the scratch is refused before it reaches the device.
+enough for several chunks (more than 4096 tokens per chunk at split 512),
+so the scratch carries the partials and the arrival flags of the chunks'
+merge.  A call whose partials exceed the scratch is refused before it
+reaches the device.
 """
 
 import pytest

@@ -75,6 +75,7 @@ SIGNATURES = {
     "spyre_kv_append_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                     c_void_p, c_int, c_int, c_int, c_int, c_int64, c_void_p]),
     "spyre_paged_decode_attn_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "spyre_paged_decode_attn_kernels": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "spyre_paged_decode_attn_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int,
                                             c_int, c_int, c_int, c_int64, c_int, c_int, c_float,

@@ -35,10 +35,14 @@ PAGE = 64
 CHUNK_WAVES = 8
 
 
-def decode_passes(max_context_len: int, split_tokens: int = 512) -> int:
-    """Kernels one decode call launches: 1, or 2 when some context may need
-    more than one chunk (the merge pass then combines the chunks)."""
-    return 1 if max_context_len <= CHUNK_WAVES * split_tokens else 2
+def decode_passes(B: int, Hq: int, Hkv: int, D: int, max_context_len: int, split_tokens: int = 512) -> int:
+    """Kernels one decode call launches on the current device: 1 when every
+    context fits one chunk or the chunks merge inside the split kernel (its
+    work list fits one round of the device), else 2 (the merge pass
+    combines the chunks)."""
+    n = _lib.lib().spyre_paged_decode_attn_kernels(B, Hq, Hkv, D, max_context_len, split_tokens)
+    _lib.check("spyre_paged_decode_attn_kernels", n if n < 0 else 0)
+    return int(n)
 
 
 def k_page_layout(num_pages: int, Hkv: int, D: int) -> SpyreTensorLayout:
@@ -210,7 +214,8 @@ class PagedDecode:
     ``merge()`` launch the two passes separately (the split pass then
     writes every chunk's partial to the workspace).  Each launch goes to the
     stream current at that moment, so the calls can be captured into a HIP
-    graph (the library allocates and clears nothing)."""
+    graph (the library allocates and clears nothing: the arrival flags of
+    chunks merged in the kernel are cleared by the call that sets them)."""
 
     def __init__(self, q, k_cache, v_cache, block_table, context_lens, scale=None,
                  split_tokens: int = 512, max_context_len: Optional[int] = None, workspace=None,
@@ -227,7 +232,7 @@ class PagedDecode:
             raise ValueError("lse must be float32 [B, Hq]")
         self.lse = lse
         self._a = a
-        self.passes = decode_passes(a.max_ctx, a.split)
+        self.passes = decode_passes(a.B, a.Hq, a.Hkv, a.D, a.max_ctx, a.split)
         L = _lib.lib()
         self._call_fn = L.spyre_paged_decode_attn_f16
         self._split_fn = L.spyre_paged_decode_attn_split_f16

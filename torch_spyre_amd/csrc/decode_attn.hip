@@ -98,9 +98,10 @@ struct SplitArgs {
   // and these strides (elements), every sequence max_ctx tokens long; q
   // [B, Hq, D] with strides q_sb, q_sh.  block_table and ctx_lens unused.
   int64_t q_sb, q_sh, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
-  // Dense K / V with several chunks per sequence: nonzero, this call's
-  // arrival-flag value (a new one per call); the chunks' partials then merge
-  // inside the kernel (run_item).  0: the merge pass combines them.
+  // Nonzero: this call's arrival-flag value (a new one per call); the
+  // chunks of a sequence with several then merge inside the kernel
+  // (run_item, merge_in_kernel), their flags after the partials in ws.
+  // 0: the merge pass combines them.
   uint32_t ticket;
 };
 
@@ -564,8 +565,8 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   l_out = l_run;
 }
 
-// Dense K / V, several chunks per sequence: after its chunk's partial (a
-// device-scope store of every element) workgroup (b, c, kvh) stores an
+// Several chunks per sequence: after its chunk's partial (a device-scope
+// store of every element) workgroup (b, c, kvh) stores an
 // arrival flag (the call's ticket) from wavefront 0, waits for it, and reads
 // the flags of every chunk of (b, kvh) with device-scope loads.  Of any two
 // workgroups, the one whose flag store finished later reads the other's
@@ -574,9 +575,12 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 // and clears the flags, so replays of a captured call (one ticket) start
 // clear and a new call's ticket matches no older call's flags.  Thread
 // (row col, features 4 d4 .. + 3), 16 chunks' loads in flight at once;
-// loads past the last chunk repeat it and carry no weight.
+// loads past the last chunk repeat it and add nothing, as in the merge
+// pass (decode_merge_kernel), whose results this matches bit for bit.
+// bad: the context broke the max_context_len contract (NaN output).
 template <int D, int W>
-__device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int nch, int wave, int lane) {
+__device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int nch, bool bad, int wave,
+                                int lane) {
   constexpr int kAuxDevice = 16;  // sc1: device scope
   constexpr int D4 = D / 4, G = 16;
   const int64_t parts = static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks;
@@ -613,25 +617,23 @@ __device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int n
         ml[jj] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, ml_off + part * 8, 0, kAuxDevice));
         ov[jj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (part * D + d) * 4, 0, kAuxDevice));
       }
-      float mv[G];  // the chunk's max, or -inf past the last chunk
-#pragma unroll
-      for (int jj = 0; jj < G; ++jj) mv[jj] = s0 + jj < nch ? ml[jj][0] : -INFINITY;
       float Mn = Mr;
 #pragma unroll
-      for (int jj = 0; jj < G; ++jj) Mn = fmaxf(Mn, mv[jj]);
+      for (int jj = 0; jj < G; ++jj)
+        if (s0 + jj < nch) Mn = fmaxf(Mn, ml[jj][0]);
       const float r = fast_exp2(Mr - Mn);  // first round: exp2(-inf) = 0
       Lr *= r;
       ac *= r;
 #pragma unroll
       for (int jj = 0; jj < G; ++jj) {
-        const float w = fast_exp2(mv[jj] - Mn);  // -inf: 0
-        Lr += ml[jj][1] * w;
-        ac += ov[jj] * w;
+        const float w = fast_exp2(ml[jj][0] - Mn);
+        Lr += s0 + jj < nch ? ml[jj][1] * w : 0.f;
+        ac += s0 + jj < nch ? ov[jj] * w : f32x4{0.f, 0.f, 0.f, 0.f};
       }
       Mr = Mn;
     }
     const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
-    const float inv = 1.f / Lr;
+    const float inv = bad ? NAN : 1.f / Lr;  // the merge pass's product, then NaN for a bad context
     f16x4 rv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) rv[e] = to_f16(ac[e] * inv);
@@ -686,42 +688,42 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
   const bool single = a.out && nch == 1;
   const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
   const int64_t slot = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks + c;
-  if constexpr (DENSE) {
-    if (!single && a.ticket) {
-      // The chunk's partial as 16-byte device-scope stores (sc1: written
-      // through to memory; the merging workgroup may run on another XCD)
-      // of 4 consecutive features per thread, then the arrival flags.  The
-      // host keeps the workspace below 2^31 bytes for this path.
-      constexpr int D4 = D / 4;
-      const Rsrc wr = __builtin_amdgcn_make_buffer_rsrc(a.ws, 0, 0x7ffffff0, kRsrcWord3);
-      const uint32_t ml_off = static_cast<uint32_t>(static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D * 4);
-      for (int u = static_cast<int>(threadIdx.x); u < a.g * D4; u += W * 64) {
-        const int col = u / D4, d0 = 4 * (u - col * D4);
-        // Features d0 .. d0 + 3 are PV row i, 4 consecutive db (the
-        // inverse of the feature map below).
-        const int i = D == 128 ? d0 >> 3 : (d0 >> 3) + 8 * ((d0 >> 2) & 1);
-        const int db0 = D == 128 ? d0 & 7 : 0;
-        const int grp = i >> 2, v = i & 3;
-        float M = -INFINITY;
+  if (!single && a.ticket) {
+    // The chunk's partial as 16-byte device-scope stores (sc1: written
+    // through to memory; the merging workgroup may run on another XCD) of 4
+    // consecutive features per thread, then the arrival flags.  The host
+    // keeps the workspace below 2^31 bytes for this path.
+    constexpr int D4 = D / 4;
+    const Rsrc wr = __builtin_amdgcn_make_buffer_rsrc(a.ws, 0, 0x7ffffff0, kRsrcWord3);
+    const uint32_t ml_off = static_cast<uint32_t>(static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D * 4);
+    for (int u = static_cast<int>(threadIdx.x); u < a.g * D4; u += W * 64) {
+      const int col = u / D4, d0 = 4 * (u - col * D4);
+      // Features d0 + e (e < 4), by the inverse of the feature map below:
+      // paged, PV row i0 + e of MFMA db0 (one f32x4 of s_o); dense, PV row
+      // i0 of MFMAs db0 + e.
+      const int i0 = !DENSE ? d0 & 15 : D == 128 ? d0 >> 3 : (d0 >> 3) + 8 * ((d0 >> 2) & 1);
+      const int db0 = !DENSE ? d0 >> 4 : D == 128 ? d0 & 7 : 0;
+      const int grp = i0 >> 2;
+      float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][col]);
-        float L = 0.f;
-        f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < W; ++w) M = fmaxf(M, s_m[w][col]);
+      float L = 0.f;
+      f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
-          const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
-          L += s_l[w][col] * sc;
+      for (int w = 0; w < W; ++w) {
+        const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
+        L += s_l[w][col] * sc;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) O[e] += s_o[w][db0 + e][grp][col][v] * sc;
-        }
-        const uint32_t part = static_cast<uint32_t>(slot * a.g + col);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), wr, (part * D + d0) * 4, 0, 16);
-        if (d0 == 0)
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), wr, ml_off + part * 8, 0, 16);
+        for (int e = 0; e < 4; ++e)
+          O[e] += (DENSE ? s_o[w][db0 + e][grp][col][i0 & 3] : s_o[w][db0][grp][col][e]) * sc;
       }
-      merge_in_kernel<D, W>(a, b, c, kvh, nch, wave, lane);
-      return;
+      const uint32_t part = static_cast<uint32_t>(slot * a.g + col);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), wr, (part * D + d0) * 4, 0, 16);
+      if (d0 == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{M, L}), wr, ml_off + part * 8, 0, 16);
     }
+    merge_in_kernel<D, W>(a, b, c, kvh, nch, bad, wave, lane);
+    return;
   }
   for (int e = static_cast<int>(threadIdx.x); e < a.g * D; e += W * 64) {
     // e -> (db, grp, col, v), v fastest, then col < g, then grp.
@@ -938,7 +940,9 @@ extern "C" size_t spyre_paged_decode_attn_workspace_bytes(int B, int Hq, int Hkv
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || split_tokens <= 0 || Hq % Hkv) return 0;
   const int64_t g = Hq / Hkv;
   const int64_t nc = max_chunks_for(max_context_len, split_tokens);
-  return static_cast<size_t>(B) * Hkv * nc * g * (D + 2) * sizeof(float);
+  // The chunk partials (fp32 O per q head and feature, m, l), then an
+  // arrival flag per (sequence, KV head, chunk) for the one-call entry.
+  return static_cast<size_t>(B) * Hkv * nc * (g * (D + 2) + 1) * sizeof(float);
 }
 
 namespace {
@@ -1052,6 +1056,16 @@ int plan_attn(const void* q, const void* k_cache, const void* v_cache, const int
   return SPYRE_OK;
 }
 
+// Whether a call of several chunks merges them inside the split kernel: its
+// work list (at most B Hkv max_chunks items) fits one round of the current
+// device's workgroup slots and the workspace (partials and flags) is
+// addressable with 32-bit offsets.
+bool merges_in_kernel(int B, int Hq, int Hkv, int D, int max_context_len, int split_tokens) {
+  const int64_t slots = split_slots(D);
+  return slots > 0 && static_cast<int64_t>(B) * Hkv * max_chunks_for(max_context_len, split_tokens) <= slots &&
+         spyre_paged_decode_attn_workspace_bytes(B, Hq, Hkv, D, max_context_len, split_tokens) < (size_t{1} << 31);
+}
+
 int launch_split(const Plan& p, hipStream_t st) {
   if (p.list && p.D == 128)
     decode_split_list_kernel<128><<<p.g1, kThreads, 0, st>>>(p.sa);
@@ -1105,6 +1119,16 @@ extern "C" int spyre_paged_decode_attn_merge_f16(const int32_t* context_lens, co
   return launch_merge(p, static_cast<hipStream_t>(stream));  // every sequence
 }
 
+extern "C" int spyre_paged_decode_attn_kernels(int B, int Hq, int Hkv, int D, int max_context_len,
+                                               int split_tokens) {
+  spyre_hip::clear_error();
+  SPYRE_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && (D == 64 || D == 128) && max_context_len >= 0 &&
+                    split_tokens > 0 && split_tokens % kPage == 0,
+                SPYRE_EINVAL, "bad decode sizes");
+  if (max_chunks_for(max_context_len, split_tokens) <= 1) return 1;
+  return merges_in_kernel(B, Hq, Hkv, D, max_context_len, split_tokens) ? 1 : 2;
+}
+
 extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* v_cache,
                                            const int32_t* block_table, int64_t bt_stride,
                                            const int32_t* context_lens, void* out, float* lse,
@@ -1119,8 +1143,18 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
                      split_tokens, scale, true, true, p);
   if (rc != SPYRE_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Several chunks: merged inside the split kernel when its work list (at
+  // most B Hkv max_chunks items) fits one round of the device's workgroup
+  // slots and the workspace (partials and flags) is addressable with 32-bit
+  // offsets; else the merge pass.  In longer lists each merging or
+  // flag-setting workgroup holds its slot through its device-scope round
+  // trips while the next item waits: B 4 x 64 / 8 heads x 131073 tokens
+  // (33 chunks, 1056 items) measured 346.5 -> 355.5 us merged in the kernel,
+  // B 1 x 32 / 8 x 131072 (264 items) 89.4 -> 88.3.
+  const bool fused = p.multi_chunk && merges_in_kernel(B, Hq, Hkv, D, max_context_len, split_tokens);
+  if (fused) p.sa.ticket = spyre_hip::next_call_ticket();
   if ((rc = launch_split(p, st)) != SPYRE_OK) return rc;
-  if (!p.multi_chunk) return SPYRE_OK;  // pass 1 wrote every output
+  if (!p.multi_chunk || fused) return SPYRE_OK;  // every output written
   p.ma.skip_single = 1;
   return launch_merge(p, st);
 }
@@ -1165,6 +1199,10 @@ DenseDecodePlan dense_decode_plan(int B, int Hq, int Hkv, int Skv, int D) {
   // Several chunks: their fp32 partials (O per q head and feature; m, l),
   // then an arrival flag per chunk (uint32).
   p.ws_bytes = p.chunks > 1 ? static_cast<size_t>(pairs) * p.chunks * ((Hq / Hkv) * (D + 2) + 1) * sizeof(float) : 0;
+  // The chunks merge in the kernel when its grid fits one round of the
+  // device's slots (as for the paged kernel) and the workspace fits 32-bit
+  // offsets; otherwise the merge pass.
+  p.fused = p.chunks > 1 && pairs * p.chunks <= (W == 4 ? slots4 : slots) && p.ws_bytes < (size_t{1} << 31);
   p.ok = true;
   return p;
 }
@@ -1205,9 +1243,7 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
   sa.v_sb = v_strides[0];
   sa.v_sh = v_strides[1];
   sa.v_ss = v_strides[2];
-  // The chunks merge inside the kernel while the workspace is addressable
-  // with 32-bit offsets; past that, in the merge pass.
-  const bool fused = plan.chunks > 1 && plan.ws_bytes < (size_t{1} << 31);
+  const bool fused = plan.fused;  // the chunks merge inside the kernel
   sa.ticket = fused ? next_call_ticket() : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(B) * Hkv * plan.chunks;

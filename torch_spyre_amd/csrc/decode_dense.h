@@ -14,6 +14,7 @@ struct DenseDecodePlan {
   int chunks = 0;       // chunks per sequence
   size_t ws_bytes = 0;  // chunks > 1: fp32 chunk partials and a flag per chunk, else 0
   int waves = 8;        // wavefronts per item (= per workgroup): 8, or 4 (twice the runs each)
+  bool fused = false;   // chunks > 1 merged inside the kernel (else the merge pass)
 };
 
 // The plan for q [B, Hq, 1, D] against K / V of Skv tokens: covered when
