@@ -713,7 +713,8 @@ def test_key_stride_near_the_descriptor_limit(cuda, Sq):
 
 # Decode calls whose (sequence, KV head, chunk) grid fills at least half the
 # device stream dense K / V through the split-KV decode kernels: one chunk
-# per sequence, or several merged in the same kernel; a ragged last 64-token run
+# per sequence, or several merged in the same kernel (the merge pass for a
+# grid of more than one round); a ragged last 64-token run
 # (read as the 64-token window ending with the last key); contexts shorter
 # than one run; g = 1 and 16; K / V rows padded past D; D = 128 and 64.
 DENSE_DECODE_CASES = [
@@ -732,7 +733,7 @@ DENSE_DECODE_CASES = [
     (32, 16, 16, 33, 8, 64),  # D = 64, shorter than one run, K / V rows 72 features apart
     (64, 32, 8, 65, 0, 128),  # the last run a window of 64 tokens with one of its own
     (64, 8, 8, 2048, 0, 128),  # four-wavefront items (the eight-wavefront grid takes two rounds)
-    (24, 32, 8, 5000, 0, 128),  # four-wavefront items in three chunks merged in the kernel
+    (24, 32, 8, 5000, 0, 128),  # four-wavefront items in three chunks, more than one round: the merge pass
 ]
 
 
