@@ -223,7 +223,8 @@ int spyre_dense_decode_load_extent(int D, int rows, int64_t k_row, int64_t v_row
 #define SPYRE_DECODE_SCRATCH_BYTES (16u << 20)
 
 /* spyre_paged_decode_attn_f16 without a workspace argument: the chunk
- * partials go to a scratch array the library holds on each GPU, so the call
+ * partials (and the arrival flags of chunks merged in the split kernel) go
+ * to a scratch array the library holds on each GPU, so the call
  * allocates nothing (no hipMalloc / hipFree, no library allocation).
  * Same arguments (less the workspace), kernels and results as
  * spyre_paged_decode_attn_f16.  Returns SPYRE_ENOSPC, before any HIP call,

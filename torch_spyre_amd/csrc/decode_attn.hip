@@ -37,9 +37,10 @@
 //
 // Pass 2 (decode_merge_kernel): per (sequence, q head) with several chunks,
 // combine the chunks' partials -- the split-KV merge -- and write fp16 out
-// (+ optional LSE).  On dense K / V (decode_dense_kernel) the chunks merge
-// in pass 1 instead: the workgroup that sees every chunk's arrival flag of
-// its (sequence, KV head) combines them (merge_in_kernel).
+// (+ optional LSE).  A one-call decode whose pass-1 grid fits one round of
+// the device's workgroup slots (paged or dense K / V) merges the chunks in
+// pass 1 instead: the workgroup that sees every chunk's arrival flag of its
+// (sequence, KV head) combines them (merge_in_kernel).
 
 #include <hip/hip_runtime.h>
 
@@ -648,8 +649,8 @@ __device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int n
 // wavefronts of the workgroup.  The wavefronts' partials are combined in LDS
 // and the whole workgroup writes the result: fp16 out and LSE when the
 // sequence has one chunk and out is given, else the chunk's partial (O per
-// q head and feature; m, l) into the workspace for the merge pass -- or, on
-// dense K / V with a ticket, for the merge in the same kernel.
+// q head and feature; m, l) into the workspace for the merge pass -- or,
+// with a ticket, for the merge in the same kernel (merge_in_kernel).
 template <int D, bool DENSE = false, int W = kWaves>
 __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int kvh, int wave,
                                          int lane) {
@@ -1383,7 +1384,9 @@ extern "C" int spyre_paged_decode_attn_noalloc_f16(const void* q, const void* k_
   void* ws = scratch_address();
   if (!ws) return SPYRE_EHIP;
   // Nothing in the scratch needs clearing: the split pass writes every
-  // partial the merge pass uses, and the merge discards the rest by selects.
+  // partial a merge uses, the merge discards the rest by selects, and the
+  // arrival flags of an in-kernel merge are cleared by the call that sets
+  // them (a new call's ticket matches no flag an older call left).
   return spyre_paged_decode_attn_f16(q, k_cache, v_cache, block_table, bt_stride, context_lens, out,
                                      lse, ws, SPYRE_DECODE_SCRATCH_BYTES, B, Hq, Hkv, D, page_size,
                                      num_pages, max_context_len, split_tokens, scale, stream);
