@@ -239,3 +239,32 @@ def test_sdpa_call_workspace_routes(tsa):
     assert need(1, [0, 0, 1, 100], 77) == 100 * 160
     # fp32 masks take V's relayout
     assert need(2, [0, 0, 160, 1], 160) == vt
+
+
+def test_paged_decode_workspace_and_kernel_count(tsa):
+    """The paged decode's workspace (host code): fp32 chunk partials
+    [B, Hkv, chunks, g, D + 2], then a 4-byte arrival flag per (sequence, KV
+    head, chunk); chunks = ceil(max_context_len / (8 split_tokens)).  The
+    kernel count of one call: 1 whenever every context fits one chunk (no
+    device is asked), a negative error code for bad sizes."""
+    from torch_spyre_amd import _lib
+
+    L = _lib.lib()
+
+    def ws(B, Hq, Hkv, D, ctx, split):
+        return L.spyre_paged_decode_attn_workspace_bytes(B, Hq, Hkv, D, ctx, split)
+
+    # Llama-3-8B decode (B 32, 32 / 8 heads, ctx 4096, split 512): one chunk
+    assert ws(32, 32, 8, 128, 4096, 512) == 32 * 8 * 1 * (4 * 130 + 1) * 4
+    # 64 sequences up to 32768 tokens: 8 chunks
+    assert ws(64, 32, 8, 128, 32768, 512) == 64 * 8 * 8 * (4 * 130 + 1) * 4
+    # B 4, 64 / 8 heads, 131073 tokens: 33 chunks of g 8
+    assert ws(4, 64, 8, 128, 131073, 512) == 4 * 8 * 33 * (8 * 130 + 1) * 4
+    # D 64, MHA, split 64: chunks of 512 tokens
+    assert ws(3, 16, 16, 64, 1025, 64) == 3 * 16 * 3 * (1 * 66 + 1) * 4
+    assert ws(0, 32, 8, 128, 4096, 512) == 0 and ws(2, 30, 8, 128, 4096, 512) == 0
+    for args in [(32, 32, 8, 128, 4096, 512), (1, 8, 8, 64, 0, 512), (6, 32, 8, 128, 2048, 256)]:
+        assert L.spyre_paged_decode_attn_kernels(*args) == 1
+    for bad in [(0, 32, 8, 128, 4096, 512), (2, 30, 8, 128, 4096, 512), (2, 32, 8, 96, 4096, 512),
+                (2, 32, 8, 128, 4096, 100), (2, 32, 8, 128, -1, 512)]:
+        assert L.spyre_paged_decode_attn_kernels(*bad) == _lib.SPYRE_EINVAL
