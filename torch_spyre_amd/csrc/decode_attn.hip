@@ -927,6 +927,68 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
   if (a.lse && d == 0) a.lse[static_cast<int64_t>(b) * a.Hq + h] = (M + log2f(L)) * kLn2;
 }
 
+// The same merge with one block per (KV head, sequence) of g D / 4 threads:
+// thread (q head col, features 4 d4 .. + 3) loads 16-byte pieces of O and
+// the (m, l) pairs of kMergeChunk chunks at once, and chunks past the
+// sequence's count repeat its last chunk instead of reading other slots.
+// Per output element the arithmetic is decode_merge_kernel's, so the two
+// give the same bits.  Needs a 16-byte aligned workspace.
+template <int D>
+__global__ __launch_bounds__(kCols * D / 4) void decode_merge_rows_kernel(MergeArgs a) {
+  constexpr int D4 = D / 4, G = kMergeChunk;
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int col = static_cast<int>(threadIdx.x) / D4, d = 4 * (static_cast<int>(threadIdx.x) % D4);
+  const int ctx_raw = a.ctx_lens ? a.ctx_lens[b] : a.max_ctx;
+  const int ctx = min(max(ctx_raw, 0), a.max_ctx);
+  const int ns = chunks_of(ctx, a.chunk_pages);
+  if (a.skip_single && ns == 1) return;
+  const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
+  _Float16* o = a.out + row * D + d;
+  if (ctx == 0) {  // empty context: zeros, as torch's CPU SDPA returns
+    *reinterpret_cast<f16x4*>(o) = f16x4{0, 0, 0, 0};
+    if (a.lse && d == 0) a.lse[row] = -INFINITY;
+    return;
+  }
+  const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks;
+  const float* wo = a.ws + (slot0 * a.g + col) * D + d;
+  const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D + (slot0 * a.g + col) * 2;
+  const int64_t so = static_cast<int64_t>(a.g) * D;  // chunk stride of wo
+  const int sm = 2 * a.g;                              // chunk stride of wm
+  float M = -INFINITY, L = 0.f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < ns; c += G) {
+    f32x2 ml[G];
+    f32x4 x[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int s = min(c + u, ns - 1);
+      ml[u] = *reinterpret_cast<const f32x2*>(wm + s * sm);
+      x[u] = *reinterpret_cast<const f32x4*>(wo + s * so);
+    }
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      if (c + u < ns) mc = fmaxf(mc, ml[u][0]);
+    const float r = fast_exp2(M - mc);  // first round: exp2(-inf) = 0
+    L *= r;
+    acc *= r;
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const float w = fast_exp2(ml[u][0] - mc);
+      L += c + u < ns ? ml[u][1] * w : 0.f;
+      acc += c + u < ns ? x[u] * w : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    M = mc;
+  }
+  const float inv = 1.f / L;
+  const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
+  f16x4 rv;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) rv[e] = to_f16(bad ? NAN : acc[e] * inv);
+  *reinterpret_cast<f16x4*>(o) = rv;
+  if (a.lse && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
+}
+
 // Chunks of the longest context: a chunk is kWaves wavefronts' shares of at
 // most split_tokens tokens each.
 int64_t max_chunks_for(int max_ctx, int split_tokens) {
@@ -1082,7 +1144,16 @@ int launch_split(const Plan& p, hipStream_t st) {
 }
 
 int launch_merge(const Plan& p, hipStream_t st) {
-  if (p.D == 128)
+  const unsigned rows_threads = static_cast<unsigned>(p.ma.g * p.D / 4);
+  // Row vectors when the workspace is 16-byte aligned: ragged batch of 64
+  // sequences 699.2 -> 695.3 us, B 32 x 32768 tokens 666.8 -> 665.2 (A/B on
+  // one box, two alternations).
+  const bool rows = reinterpret_cast<uintptr_t>(p.ma.ws) % 16 == 0;
+  if (rows && p.D == 128)
+    decode_merge_rows_kernel<128><<<dim3(p.ma.Hkv, p.ma.B), rows_threads, 0, st>>>(p.ma);
+  else if (rows)
+    decode_merge_rows_kernel<64><<<dim3(p.ma.Hkv, p.ma.B), rows_threads, 0, st>>>(p.ma);
+  else if (p.D == 128)
     decode_merge_kernel<128><<<p.g2, 128, 0, st>>>(p.ma);
   else
     decode_merge_kernel<64><<<p.g2, 64, 0, st>>>(p.ma);
@@ -1261,10 +1332,11 @@ int dense_decode_launch(const DenseDecodePlan& plan, const void* q, const int64_
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode launch failed: %s", hipGetErrorString(e));
   if (plan.chunks == 1 || fused) return SPYRE_OK;  // every sequence's output written
   const MergeArgs ma{sa.ws, nullptr, sa.out, lse, B, Hq, Hkv, sa.g, plan.chunks, plan.chunk_pages, Skv, 0};
+  // The workspace is 16-byte aligned on this route (the SDPA entry checks).
   if (D == 128)
-    decode_merge_kernel<128><<<dim3(Hq, B), 128, 0, st>>>(ma);
+    decode_merge_rows_kernel<128><<<dim3(Hkv, B), sa.g * 128 / 4, 0, st>>>(ma);
   else
-    decode_merge_kernel<64><<<dim3(Hq, B), 64, 0, st>>>(ma);
+    decode_merge_rows_kernel<64><<<dim3(Hkv, B), sa.g * 64 / 4, 0, st>>>(ma);
   e = hipGetLastError();
   SPYRE_REQUIRE(e == hipSuccess, SPYRE_EHIP, "dense decode merge launch failed: %s", hipGetErrorString(e));
   return SPYRE_OK;
