@@ -52,7 +52,7 @@ PEAK_HBM_GBS = 8000.0
 # counters on torch's 32 MiB device copy (x1.99860 and x1.0): 536.99 MB read
 # + 0.26 MB written (profiles/decode_attention_llama3_8b_b32_ctx4096_hbm_counters.md).
 # Re-measure both together whenever decode_split_list_kernel changes.
-TRAFFIC_BYTES = 537_255_236
+TRAFFIC_BYTES = 537_251_143
 B, HQ, HKV, D, CTX, PAGE, SPLIT = 32, 32, 8, 128, 4096, 64, 512
 
 
