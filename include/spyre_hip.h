@@ -181,8 +181,8 @@ int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, const void* 
 /* Kernels one spyre_paged_decode_attn_f16 call of these sizes launches on
  * the current device: 1 when every context fits one chunk or the chunks
  * merge inside the split kernel (its work list, B * Hkv * chunks items, fits
- * one round of the device's workgroup slots), else 2; negative on bad
- * sizes.  No reference counterpart (a helper for callers that account
+ * one round of the device's workgroup slots, and the workspace is 16-byte
+ * aligned), else 2; negative on bad sizes.  No reference counterpart (a helper for callers that account
  * kernels per step). */
 int spyre_paged_decode_attn_kernels(int B, int Hq, int Hkv, int D, int max_context_len, int split_tokens);
 

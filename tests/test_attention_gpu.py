@@ -429,6 +429,29 @@ def test_chunks_merge_in_kernel_or_pass(cuda, B, kernels):
     assert_close(one, oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128)))
 
 
+def test_workspace_alignment_paths_agree(cuda):
+    """A 16-byte aligned workspace (two-chunk contexts merged inside the
+    split kernel) and one 4 bytes off it (the merge pass with scalar loads)
+    give the same bits, output and LSE; both against the oracle."""
+    import torch_spyre_amd as tsa
+
+    lens = [5000, 700, 64, 4097]
+    B = len(lens)
+    cache, table, lens_t, q = make_case(cuda, B, 32, 8, 128, lens, SEED + 49)
+    t, l = table.to(cuda), lens_t.to(cuda)
+    need = tsa.workspace_bytes(B, 32, 8, 128, max(lens), 256)
+    buf = torch.empty(need + 64, dtype=torch.uint8, device=cuda)
+    res = []
+    for off in (0, 4):
+        ws = buf[off:off + need]
+        assert ws.data_ptr() % 16 == off
+        res.append(tsa.paged_decode_attention(q, cache.k, cache.v, t, l, split_tokens=256, max_context_len=max(lens),
+                                              workspace=ws, return_lse=True))
+    assert torch.equal(res[0][0].view(torch.int16), res[1][0].view(torch.int16))
+    assert torch.equal(res[0][1], res[1][1])
+    assert_close(res[0][0], oracle_rows(cache, table, lens_t, q, list(range(B)), 1 / math.sqrt(128)))
+
+
 @pytest.mark.parametrize("split", [512, 256])
 def test_context_past_max_gives_nan_rows(cuda, split):
     """A context longer than max_context_len breaks the call's contract: the

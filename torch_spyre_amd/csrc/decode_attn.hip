@@ -1217,13 +1217,15 @@ extern "C" int spyre_paged_decode_attn_f16(const void* q, const void* k_cache, c
   hipStream_t st = static_cast<hipStream_t>(stream);
   // Several chunks: merged inside the split kernel when its work list (at
   // most B Hkv max_chunks items) fits one round of the device's workgroup
-  // slots and the workspace (partials and flags) is addressable with 32-bit
-  // offsets; else the merge pass.  In longer lists each merging or
+  // slots and the workspace (partials and flags, moved as 16-byte pieces)
+  // is 16-byte aligned and addressable with 32-bit offsets; else the merge
+  // pass.  In longer lists each merging or
   // flag-setting workgroup holds its slot through its device-scope round
   // trips while the next item waits: B 4 x 64 / 8 heads x 131073 tokens
   // (33 chunks, 1056 items) measured 346.5 -> 355.5 us merged in the kernel,
   // B 1 x 32 / 8 x 131072 (264 items) 89.4 -> 88.3.
-  const bool fused = p.multi_chunk && merges_in_kernel(B, Hq, Hkv, D, max_context_len, split_tokens);
+  const bool fused = p.multi_chunk && reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                     merges_in_kernel(B, Hq, Hkv, D, max_context_len, split_tokens);
   if (fused) p.sa.ticket = spyre_hip::next_call_ticket();
   if ((rc = launch_split(p, st)) != SPYRE_OK) return rc;
   if (!p.multi_chunk || fused) return SPYRE_OK;  // every output written
