@@ -233,6 +233,8 @@ class PagedDecode:
         self.lse = lse
         self._a = a
         self.passes = decode_passes(a.B, a.Hq, a.Hkv, a.D, a.max_ctx, a.split)
+        if a.ws.data_ptr() % 16 and a.max_ctx > CHUNK_WAVES * a.split:
+            self.passes = 2  # a workspace aligned to less than 16 bytes takes the merge pass
         L = _lib.lib()
         self._call_fn = L.spyre_paged_decode_attn_f16
         self._split_fn = L.spyre_paged_decode_attn_split_f16
