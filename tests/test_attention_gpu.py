@@ -400,21 +400,21 @@ def test_two_pass_api_equals_single_call_bitexact(cuda, lens):
     assert torch.equal(lse1, lse2)
 
 
-@pytest.mark.parametrize("B,kernels", [(7, 1), (40, 2)], ids=str)
-def test_chunks_merge_in_kernel_or_pass(cuda, B, kernels):
+@pytest.mark.parametrize("B,kernels,D", [(7, 1, 128), (40, 2, 128), (7, 1, 64), (40, 2, 64)], ids=str)
+def test_chunks_merge_in_kernel_or_pass(cuda, B, kernels, D):
     """Contexts of up to three 2048-token chunks (split 256).  7 sequences x
     8 KV heads x 3 chunks fit one round of a 256-CU device's workgroups, so
     the chunks merge inside the split kernel (one kernel); 40 sequences take
     four rounds and the merge pass.  Both bit-equal to the two-pass API
-    (split, then the merge pass), every row against the oracle."""
+    (split, then the merge pass), every row against the oracle; D 128 and 64."""
     import torch_spyre_amd as tsa
     from torch_spyre_amd import _lib
 
     if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
         pytest.skip("the kernel counts assume a 256-CU device")
     lens = ([5000, 700, 64, 4097, 2049, 1, 6000] * 6)[:B]
-    assert _lib.lib().spyre_paged_decode_attn_kernels(B, 32, 8, 128, max(lens), 256) == kernels
-    cache, table, lens_t, q = make_case(cuda, B, 32, 8, 128, lens, SEED + 43 + B)
+    assert _lib.lib().spyre_paged_decode_attn_kernels(B, 32, 8, D, max(lens), 256) == kernels
+    cache, table, lens_t, q = make_case(cuda, B, 32, 8, D, lens, SEED + 43 + B + D)
     t, l = table.to(cuda), lens_t.to(cuda)
     call = tsa.PagedDecode(q, cache.k, cache.v, t, l, split_tokens=256, max_context_len=max(lens),
                            lse=torch.empty((B, 32), dtype=torch.float32, device=cuda))
@@ -426,7 +426,7 @@ def test_chunks_merge_in_kernel_or_pass(cuda, B, kernels):
     assert torch.equal(one.view(torch.int16), two.view(torch.int16))
     assert torch.equal(lse1, call.lse)
     rows = list(range(B))
-    assert_close(one, oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(128)))
+    assert_close(one, oracle_rows(cache, table, lens_t, q, rows, 1 / math.sqrt(D)))
 
 
 def test_workspace_alignment_paths_agree(cuda):
