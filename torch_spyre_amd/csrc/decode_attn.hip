@@ -566,6 +566,53 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
   l_out = l_run;
 }
 
+// Chunks whose loads are issued together in a merge (one memory latency
+// for up to this many chunks).
+constexpr int kMergeChunk = 16;
+
+// The merge of one output row's 4 features over a sequence's nch chunk
+// partials, the split-KV merge of both the merge pass and the in-kernel
+// merge: load_ml(s) / load_o(s) return chunk s's (m, l) and the row's 4
+// features of O.  kMergeChunk chunks' loads go out together; past the last
+// chunk the loads repeat it and add nothing.  Running (M, L, acc) as the
+// online softmax rescales them; returns acc and leaves M, L.
+template <typename LoadML, typename LoadO>
+__device__ __forceinline__ f32x4 merge_row4(int nch, LoadML load_ml, LoadO load_o, float& M, float& L) {
+  constexpr int G = kMergeChunk;
+  M = -INFINITY;
+  L = 0.f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nch; c += G) {
+    f32x2 ml[G];
+    f32x4 x[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int s = min(c + u, nch - 1);
+      ml[u] = load_ml(s);
+      x[u] = load_o(s);
+    }
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      if (c + u < nch) mc = fmaxf(mc, ml[u][0]);
+    const float r = fast_exp2(M - mc);  // first round: exp2(-inf) = 0
+    L *= r;
+    acc *= r;
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      // Explicit fused multiply-adds: every kernel that merges rounds alike.
+      const float w = fast_exp2(ml[u][0] - mc);
+      if (c + u < nch) {
+        L = __builtin_fmaf(ml[u][1], w, L);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[u][e], w, acc[e]);
+      }
+    }
+    M = mc;
+  }
+  return acc;
+}
+
 // Several chunks per sequence: after its chunk's partial (a device-scope
 // store of every element) workgroup (b, c, kvh) stores an
 // arrival flag (the call's ticket) from wavefront 0, waits for it, and reads
@@ -575,15 +622,14 @@ __device__ __forceinline__ void stream_pages(const SplitArgs& a, int b, int kvh,
 // merges the g rows of (b, kvh) over the chunks in order (to the same bits)
 // and clears the flags, so replays of a captured call (one ticket) start
 // clear and a new call's ticket matches no older call's flags.  Thread
-// (row col, features 4 d4 .. + 3), 16 chunks' loads in flight at once;
-// loads past the last chunk repeat it and add nothing, as in the merge
-// pass (decode_merge_kernel), whose results this matches bit for bit.
-// bad: the context broke the max_context_len contract (NaN output).
+// (row col, features 4 d4 .. + 3) merges by merge_row4 with device-scope
+// loads, so its results match the merge pass's bit for bit.  bad: the
+// context broke the max_context_len contract (NaN output).
 template <int D, int W>
 __device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int nch, bool bad, int wave,
                                 int lane) {
   constexpr int kAuxDevice = 16;  // sc1: device scope
-  constexpr int D4 = D / 4, G = 16;
+  constexpr int D4 = D / 4;
   const int64_t parts = static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks;
   const int64_t slot0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * a.max_chunks;
   const Rsrc wr = __builtin_amdgcn_make_buffer_rsrc(a.ws, 0, 0x7ffffff0, kRsrcWord3);
@@ -603,36 +649,21 @@ __device__ void merge_in_kernel(const SplitArgs& a, int b, int c, int kvh, int n
   __syncthreads();
   if (!s_merge) return;
   const uint32_t ml_off = static_cast<uint32_t>(parts * a.g * D * 4);
-  const uint32_t last = static_cast<uint32_t>(nch - 1);
   for (int u = static_cast<int>(threadIdx.x); u < a.g * D4; u += W * 64) {
     const int col = u / D4, d = 4 * (u - col * D4);
-    float Mr = -INFINITY, Lr = 0.f;
-    f32x4 ac = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nch; s0 += G) {
-      f32x2 ml[G];
-      f32x4 ov[G];
-#pragma unroll
-      for (int jj = 0; jj < G; ++jj) {
-        const uint32_t s2 = min(static_cast<uint32_t>(s0 + jj), last);
-        const uint32_t part = static_cast<uint32_t>((slot0 + s2) * a.g + col);
-        ml[jj] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, ml_off + part * 8, 0, kAuxDevice));
-        ov[jj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (part * D + d) * 4, 0, kAuxDevice));
-      }
-      float Mn = Mr;
-#pragma unroll
-      for (int jj = 0; jj < G; ++jj)
-        if (s0 + jj < nch) Mn = fmaxf(Mn, ml[jj][0]);
-      const float r = fast_exp2(Mr - Mn);  // first round: exp2(-inf) = 0
-      Lr *= r;
-      ac *= r;
-#pragma unroll
-      for (int jj = 0; jj < G; ++jj) {
-        const float w = fast_exp2(ml[jj][0] - Mn);
-        Lr += s0 + jj < nch ? ml[jj][1] * w : 0.f;
-        ac += s0 + jj < nch ? ov[jj] * w : f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      Mr = Mn;
-    }
+    const uint32_t part0 = static_cast<uint32_t>(slot0 * a.g + col);  // chunk s: part0 + s g
+    float Mr, Lr;
+    const f32x4 ac = merge_row4(
+        nch,
+        [&](int s) {
+          const uint32_t part = part0 + static_cast<uint32_t>(s * a.g);
+          return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, ml_off + part * 8, 0, kAuxDevice));
+        },
+        [&](int s) {
+          const uint32_t part = part0 + static_cast<uint32_t>(s * a.g);
+          return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (part * D + d) * 4, 0, kAuxDevice));
+        },
+        Mr, Lr);
     const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
     const float inv = bad ? NAN : 1.f / Lr;  // the merge pass's product, then NaN for a bad context
     f16x4 rv;
@@ -874,7 +905,6 @@ struct MergeArgs {
 // they cost one memory latency; chunks past the sequence's count are read
 // (in bounds: the workspace holds max_chunks) and discarded by selects,
 // never multiplied.
-constexpr int kMergeChunk = 16;
 
 template <int D>
 __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
@@ -915,9 +945,11 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
     acc *= r;
 #pragma unroll
     for (int u = 0; u < kMergeChunk; ++u) {
-      const float w = fast_exp2(m[u] - mc);
-      L += c + u < ns ? l[u] * w : 0.f;
-      acc += c + u < ns ? x[u] * w : 0.f;
+      const float w = fast_exp2(m[u] - mc);  // fused multiply-adds, as merge_row4
+      if (c + u < ns) {
+        L = __builtin_fmaf(l[u], w, L);
+        acc = __builtin_fmaf(x[u], w, acc);
+      }
     }
     M = mc;
   }
@@ -928,14 +960,14 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(MergeArgs a) {
 }
 
 // The same merge with one block per (KV head, sequence) of g D / 4 threads:
-// thread (q head col, features 4 d4 .. + 3) loads 16-byte pieces of O and
-// the (m, l) pairs of kMergeChunk chunks at once, and chunks past the
-// sequence's count repeat its last chunk instead of reading other slots.
-// Per output element the arithmetic is decode_merge_kernel's, so the two
-// give the same bits.  Needs a 16-byte aligned workspace.
+// thread (q head col, features 4 d4 .. + 3) merges by merge_row4, loading
+// 16-byte pieces of O, and chunks past the sequence's count repeat its last
+// chunk instead of reading other slots.  Per output element the arithmetic
+// is decode_merge_kernel's, so the two give the same bits.  Needs a 16-byte
+// aligned workspace.
 template <int D>
 __global__ __launch_bounds__(kCols * D / 4) void decode_merge_rows_kernel(MergeArgs a) {
-  constexpr int D4 = D / 4, G = kMergeChunk;
+  constexpr int D4 = D / 4;
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int col = static_cast<int>(threadIdx.x) / D4, d = 4 * (static_cast<int>(threadIdx.x) % D4);
   const int ctx_raw = a.ctx_lens ? a.ctx_lens[b] : a.max_ctx;
@@ -954,32 +986,10 @@ __global__ __launch_bounds__(kCols * D / 4) void decode_merge_rows_kernel(MergeA
   const float* wm = a.ws + static_cast<int64_t>(a.B) * a.Hkv * a.max_chunks * a.g * D + (slot0 * a.g + col) * 2;
   const int64_t so = static_cast<int64_t>(a.g) * D;  // chunk stride of wo
   const int sm = 2 * a.g;                              // chunk stride of wm
-  float M = -INFINITY, L = 0.f;
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < ns; c += G) {
-    f32x2 ml[G];
-    f32x4 x[G];
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const int s = min(c + u, ns - 1);
-      ml[u] = *reinterpret_cast<const f32x2*>(wm + s * sm);
-      x[u] = *reinterpret_cast<const f32x4*>(wo + s * so);
-    }
-    float mc = M;
-#pragma unroll
-    for (int u = 0; u < G; ++u)
-      if (c + u < ns) mc = fmaxf(mc, ml[u][0]);
-    const float r = fast_exp2(M - mc);  // first round: exp2(-inf) = 0
-    L *= r;
-    acc *= r;
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const float w = fast_exp2(ml[u][0] - mc);
-      L += c + u < ns ? ml[u][1] * w : 0.f;
-      acc += c + u < ns ? x[u] * w : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    M = mc;
-  }
+  float M, L;
+  const f32x4 acc = merge_row4(
+      ns, [&](int s) { return *reinterpret_cast<const f32x2*>(wm + s * sm); },
+      [&](int s) { return *reinterpret_cast<const f32x4*>(wo + s * so); }, M, L);
   const float inv = 1.f / L;
   const bool bad = ctx_raw > a.max_ctx;  // caller broke the max_context_len contract
   f16x4 rv;
