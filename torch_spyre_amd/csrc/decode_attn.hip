@@ -744,10 +744,10 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
 #pragma unroll
       for (int w = 0; w < W; ++w) {
         const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
-        L += s_l[w][col] * sc;
+        L = __builtin_fmaf(s_l[w][col], sc, L);  // as the per-element fold below
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          O[e] += (DENSE ? s_o[w][db0 + e][grp][col][i0 & 3] : s_o[w][db0][grp][col][e]) * sc;
+          O[e] = __builtin_fmaf(DENSE ? s_o[w][db0 + e][grp][col][i0 & 3] : s_o[w][db0][grp][col][e], sc, O[e]);
       }
       const uint32_t part = static_cast<uint32_t>(slot * a.g + col);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), wr, (part * D + d0) * 4, 0, 16);
@@ -773,8 +773,10 @@ __device__ __forceinline__ void run_item(const SplitArgs& a, int b, int c, int k
     for (int w = 0; w < W; ++w) {
       // Empty partials (m = -inf) weigh 0; all empty: M = -inf, L = O = 0.
       const float sc = M == -INFINITY ? 0.f : fast_exp2(s_m[w][col] - M);
-      L += s_l[w][col] * sc;
-      O += s_o[w][db][grp][col][v] * sc;
+      // Explicit fused multiply-adds: the partials of the vector path above
+      // (chunks merged in the kernel) and of this one round alike.
+      L = __builtin_fmaf(s_l[w][col], sc, L);
+      O = __builtin_fmaf(s_o[w][db][grp][col][v], sc, O);
     }
     if (single) {
       const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * a.g + col;
