@@ -1591,7 +1591,11 @@ __global__ __launch_bounds__(256) void sdpa_split_merge_rows_kernel(MergeArgs a)
       const int sp = s0 + j;
       const bool in = sp < a.nsplit;
       ml[j] = in ? *reinterpret_cast<const f32x2*>(pml + 2 * sp) : f32x2{-INFINITY, 0.f};
-      ov[j] = in ? *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(sp) * D) : f32x4{0.f, 0.f, 0.f, 0.f};
+      // Non-temporal: each partial is read once (chunked prefill, B 4 x 128
+      // queries x 4096 keys, 56.2 -> 55.3 us a call; B 8 x 64 x 4096 56.7 ->
+      // 52.9 us; one box, two alternations).
+      ov[j] = in ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(sp) * D))
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float Mn = M;
 #pragma unroll
